@@ -1,0 +1,25 @@
+"""MI355X-native GPTQ hot path behind the Python API of
+kambojvikram/Distributed_GPTQ (src/distributed_gptq/__init__.py:11-31).
+
+Compute runs in libgptq_hip.so (hand-written gfx950 HIP kernels behind a
+C ABI, include/gptq_hip.h); this package mirrors the reference's import
+paths: ``core.gptq`` (GPTQ), ``core.quantizer`` (QuantizationConfig,
+Quantizer), ``core.dequantizer``, ``models.layers`` (QuantizedLinear and the
+gptq::linear operator) and ``kernels``.
+"""
+from .core.gptq import GPTQ, GPTQMultiGPU, quantize_layer_gptq
+from .core.quantizer import QuantizationConfig, Quantizer
+from .core.dequantizer import GPTQDequantizer
+
+__version__ = "0.1.0"
+
+__all__ = ["GPTQ", "GPTQMultiGPU", "quantize_layer_gptq", "QuantizationConfig", "Quantizer", "GPTQDequantizer",
+           "QuantizedLinear", "replace_with_quantized_layers"]
+
+
+def __getattr__(name):
+    # models.layers registers the gptq::linear operator on import
+    if name in ("QuantizedLinear", "replace_with_quantized_layers"):
+        from .models import layers
+        return getattr(layers, name)
+    raise AttributeError(name)

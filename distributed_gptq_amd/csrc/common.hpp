@@ -1,0 +1,81 @@
+// Shared helpers of libgptq_hip.so: status/last-error plumbing, element
+// conversions and the MFMA vector types used by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/gptq_hip.h"
+
+namespace gptq {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// -------------------------------------------------------------- errors ----
+void set_error(const char* fmt, ...);
+void clear_error();
+
+inline hipStream_t as_hip(gptq_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+#define GPTQ_REQUIRE(cond, code, ...)   \
+  do {                                  \
+    if (!(cond)) {                      \
+      ::gptq::set_error(__VA_ARGS__);   \
+      return (code);                    \
+    }                                   \
+  } while (0)
+
+// Checks the launch just enqueued.
+int check_launch(const char* what);
+
+// ----------------------------------------------------- element access ----
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+  _Float16 h;
+  __builtin_memcpy(&h, &b, 2);
+  return static_cast<float>(h);
+}
+// Round-to-nearest-even float -> bf16 bits (inputs here are finite).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u) return static_cast<uint16_t>((u >> 16) | ((u & 0xffff) ? 0x40 : 0));
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  _Float16 h = static_cast<_Float16>(f);
+  uint16_t b;
+  __builtin_memcpy(&b, &h, 2);
+  return b;
+}
+
+__device__ __forceinline__ float load_elem(const void* p, int64_t i, int dtype) {
+  if (dtype == GPTQ_F32) return static_cast<const float*>(p)[i];
+  uint16_t b = static_cast<const uint16_t*>(p)[i];
+  return dtype == GPTQ_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+}
+__device__ __forceinline__ void store_elem(void* p, int64_t i, int dtype, float v) {
+  if (dtype == GPTQ_F32) {
+    static_cast<float*>(p)[i] = v;
+  } else {
+    static_cast<uint16_t*>(p)[i] = dtype == GPTQ_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
+  }
+}
+
+inline bool valid_dtype(int d) { return d == GPTQ_F32 || d == GPTQ_F16 || d == GPTQ_BF16; }
+inline int dtype_size(int d) { return d == GPTQ_F32 ? 4 : 2; }
+__host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace gptq

@@ -1,0 +1,457 @@
+// Dequant-matmul y = x @ dequant(W)^T (+ bias) on gfx950: the gptq::linear op.
+//
+// Weight rows are the native LSB-first bit streams (pitch ceil(K*bits/8)),
+// scales/zeros (N x ngroups), group of column k = k / group_size (or g_idx).
+// sum_k x_k (q_k - z) s is evaluated per chunk as s * (sum_k x_k q_k -
+// z * sum_k x_k) with exact small-integer codes in fp16/bf16 and fp32
+// accumulation, so a code costs one packed decode step and half a v_dot2.
+//
+//  * gemv_k (M <= 4): 4 waves per workgroup share x staged in LDS; a wave
+//    walks 4 weight rows at a time, lane l taking 128-bit chunks l, l+64, ...
+//    of each row (a wave load covers 1 KiB of contiguous codes).  Within a
+//    chunk, codes are paired the way the packed word yields them cheaply
+//    ((0,4),(1,5).. for 4-bit), and x is stored in LDS in that order.
+//  * dq_mfma_k (larger M): v_mfma_f32_16x16x32_{f16,bf16} on 16 weight rows x
+//    16 activation rows per step, 4 waves splitting K; partial sums reduced in
+//    LDS.
+//  * linear_generic: any layout (fp32 x, g_idx, ragged K): one wave per
+//    output, fp32.
+#include "common.hpp"
+
+namespace gptq {
+namespace {
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <int BITS> struct Fmt;
+template <> struct Fmt<4> { static constexpr int CB = 32, NW = 4; };
+template <> struct Fmt<2> { static constexpr int CB = 64, NW = 4; };
+template <> struct Fmt<8> { static constexpr int CB = 16, NW = 4; };
+template <> struct Fmt<3> { static constexpr int CB = 128, NW = 12; };
+
+// chunk-local code index held by LDS slot s (pairs of slots = decoded pairs)
+template <int BITS>
+__device__ __forceinline__ int slot_code(int s) {
+  if constexpr (BITS == 4) {
+    const int d = s >> 3, j = s & 7;
+    return 8 * d + (j >> 1) + 4 * (j & 1);
+  } else if constexpr (BITS == 2) {
+    const int d = s >> 4, j = s & 15;
+    return 16 * d + (j >> 1) + 8 * (j & 1);
+  } else {
+    return s;
+  }
+}
+
+// codes of pair p of a chunk as two 16-bit integers (lo, hi)
+template <int BITS, int P>
+__device__ __forceinline__ uint32_t decode_pair(const uint32_t* dw) {
+  if constexpr (BITS == 4) {
+    constexpr int d = P / 4, i = P % 4;
+    return (dw[d] >> (4 * i)) & 0x000F000Fu;
+  } else if constexpr (BITS == 2) {
+    constexpr int d = P / 8, i = P % 8;
+    return (dw[d] >> (2 * i)) & 0x00030003u;
+  } else if constexpr (BITS == 8) {
+    constexpr int d = P / 2, i = P % 2;
+    const uint32_t w = dw[d] >> (16 * i);
+    return (w & 0xFFu) | ((w & 0xFF00u) << 8);
+  } else {
+    constexpr int b0 = 6 * P;  // bit offset of code 2P
+    constexpr int d = b0 / 32, o = b0 % 32;
+    uint64_t v = dw[d];
+    if constexpr (d + 1 < Fmt<3>::NW) v |= static_cast<uint64_t>(dw[d + 1]) << 32;
+    v >>= o;
+    return static_cast<uint32_t>(v & 7u) | (static_cast<uint32_t>((v >> 3) & 7u) << 16);
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// dot of the chunk's decoded codes with x pairs; returns sum x*(code + bias)
+// where bias = 0 (fp16: exact packed subtraction of the 1024 magic) or 128
+// (bf16: the magic is left in and corrected by the caller).
+template <int BITS, bool BF16, int P>
+__device__ __forceinline__ float chunk_dot_pair(const uint32_t* dw, uint32_t xpair, float acc) {
+  const uint32_t c = decode_pair<BITS, P>(dw);
+  if constexpr (!BF16) {
+    const uint32_t t = c | 0x64006400u;                 // 1024 + code, fp16
+    f16x2 h = __builtin_bit_cast(f16x2, t) - f16x2{1024.0f16, 1024.0f16};
+    return __builtin_amdgcn_fdot2(h, __builtin_bit_cast(f16x2, xpair), acc, false);
+  } else {
+    const uint32_t t = c | 0x43004300u;                 // 128 + code, bf16
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, t), __builtin_bit_cast(bf16x2, xpair), acc,
+                                           false);
+  }
+}
+
+template <int BITS, bool BF16, int... Ps>
+__device__ __forceinline__ float chunk_dot(const uint32_t* dw, const uint32_t* xp, std::integer_sequence<int, Ps...>) {
+  float acc = 0.0f;
+  ((acc = chunk_dot_pair<BITS, BF16, Ps>(dw, xp[Ps], acc)), ...);
+  return acc;
+}
+
+struct LinArgs {
+  const uint16_t* x;
+  int64_t M;
+  const uint8_t* packed;
+  int64_t pitch;
+  const void* scales;
+  const void* zeros;
+  int sz_dtype;
+  int gs;
+  int64_t ngroups;
+  const void* bias;
+  int bias_dtype;
+  int64_t N, K;
+  uint16_t* y;
+  int y_dtype;
+};
+
+constexpr int kRB = 4;  // weight rows per wave pass
+
+template <int BITS, bool BF16, int MV>
+__global__ __launch_bounds__(256) void gemv_k(LinArgs a) {
+  using F = Fmt<BITS>;
+  constexpr int CB = F::CB;
+  constexpr int NP = CB / 2;  // pairs per chunk
+  extern __shared__ uint32_t lds[];
+  const int64_t K = a.K;
+  const int64_t nch = K / CB;
+  uint16_t* xs = reinterpret_cast<uint16_t*>(lds);          // MV x K (slot order)
+  float* xsum = reinterpret_cast<float*>(lds + MV * K / 2);  // MV x nch
+  const int tid = threadIdx.x;
+  for (int64_t i = tid; i < MV * K; i += 256) {
+    const int64_t m = i / K, s = i - (i / K) * K;
+    const int64_t c = s / CB;
+    const int cs = static_cast<int>(s - c * CB);
+    xs[i] = a.x[m * K + c * CB + slot_code<BITS>(cs)];
+  }
+  __syncthreads();
+  for (int64_t i = tid; i < MV * nch; i += 256) {
+    const int64_t m = i / nch, c = i - (i / nch) * nch;
+    float s = 0.0f;
+    for (int e = 0; e < CB; ++e) {
+      const uint16_t b = xs[m * K + c * CB + e];
+      s += BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+    }
+    xsum[i] = s;
+  }
+  __syncthreads();
+
+  const int lane = tid & 63;
+  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * 4;
+  const int64_t nbatches = cdiv(a.N, kRB);
+  for (int64_t rb = blockIdx.x * 4LL + (tid >> 6); rb < nbatches; rb += nwaves) {
+    const int64_t n0 = rb * kRB;
+    float acc[kRB][MV];
+#pragma unroll
+    for (int r = 0; r < kRB; ++r)
+#pragma unroll
+      for (int m = 0; m < MV; ++m) acc[r][m] = 0.0f;
+#pragma unroll 2
+    for (int64_t c = lane; c < nch; c += 64) {
+      uint32_t dw[kRB][F::NW];
+#pragma unroll
+      for (int r = 0; r < kRB; ++r) {
+        const int64_t n = std::min<int64_t>(n0 + r, a.N - 1);
+        const u32x4* src = reinterpret_cast<const u32x4*>(a.packed + n * a.pitch + c * (CB * BITS / 8));
+#pragma unroll
+        for (int v = 0; v < F::NW / 4; ++v) {
+          const u32x4 t = __builtin_nontemporal_load(src + v);
+          dw[r][4 * v] = t[0]; dw[r][4 * v + 1] = t[1]; dw[r][4 * v + 2] = t[2]; dw[r][4 * v + 3] = t[3];
+        }
+      }
+      const int64_t g = (c * CB) / a.gs;
+      float sc[kRB], zc[kRB];
+#pragma unroll
+      for (int r = 0; r < kRB; ++r) {
+        const int64_t n = std::min<int64_t>(n0 + r, a.N - 1);
+        sc[r] = load_elem(a.scales, n * a.ngroups + g, a.sz_dtype);
+        zc[r] = load_elem(a.zeros, n * a.ngroups + g, a.sz_dtype);
+        if constexpr (BF16) zc[r] += 128.0f;
+      }
+#pragma unroll
+      for (int m = 0; m < MV; ++m) {
+        uint32_t xp[NP];
+        const u32x4* xv = reinterpret_cast<const u32x4*>(xs + m * K + c * CB);
+#pragma unroll
+        for (int v = 0; v < NP / 4; ++v) {
+          const u32x4 t = xv[v];
+          xp[4 * v] = t[0]; xp[4 * v + 1] = t[1]; xp[4 * v + 2] = t[2]; xp[4 * v + 3] = t[3];
+        }
+        const float xsm = xsum[m * nch + c];
+#pragma unroll
+        for (int r = 0; r < kRB; ++r) {
+          const float d = chunk_dot<BITS, BF16>(dw[r], xp, std::make_integer_sequence<int, NP>{});
+          acc[r][m] += sc[r] * (d - zc[r] * xsm);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kRB; ++r)
+#pragma unroll
+      for (int m = 0; m < MV; ++m) acc[r][m] = wave_sum(acc[r][m]);
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < kRB; ++r) {
+        const int64_t n = n0 + r;
+        if (n >= a.N) continue;
+        const float b = a.bias ? load_elem(a.bias, n, a.bias_dtype) : 0.0f;
+#pragma unroll
+        for (int m = 0; m < MV; ++m) store_elem(a.y, m * a.N + n, a.y_dtype, acc[r][m] + b);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------ MFMA path ----
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// 8 consecutive codes (natural order) of a row at code index k (k % 8 == 0)
+template <int BITS>
+__device__ __forceinline__ void load8(const uint8_t* row, int64_t k, uint32_t (&c)[4]) {
+  uint32_t w0 = 0, w1 = 0;
+  if constexpr (BITS == 4) {
+    w0 = *reinterpret_cast<const uint32_t*>(row + k / 2);
+    c[0] = (w0 & 0xFu) | ((w0 & 0xF0u) << 12);
+    c[1] = ((w0 >> 8) & 0xFu) | ((w0 & 0xF000u) << 4);
+    c[2] = ((w0 >> 16) & 0xFu) | ((w0 >> 4) & 0xF0000u);
+    c[3] = ((w0 >> 24) & 0xFu) | ((w0 >> 12) & 0xF0000u);
+  } else if constexpr (BITS == 2) {
+    w0 = *reinterpret_cast<const uint16_t*>(row + k / 4);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) c[p] = ((w0 >> (4 * p)) & 3u) | (((w0 >> (4 * p + 2)) & 3u) << 16);
+  } else if constexpr (BITS == 8) {
+    const u32x2 v = *reinterpret_cast<const u32x2*>(row + k);
+    w0 = v[0];
+    w1 = v[1];
+    c[0] = (w0 & 0xFFu) | ((w0 & 0xFF00u) << 8);
+    c[1] = ((w0 >> 16) & 0xFFu) | ((w0 >> 8) & 0xFF0000u);
+    c[2] = (w1 & 0xFFu) | ((w1 & 0xFF00u) << 8);
+    c[3] = ((w1 >> 16) & 0xFFu) | ((w1 >> 8) & 0xFF0000u);
+  } else {
+    const uint8_t* p = row + (k * 3) / 8;
+    const uint32_t v = p[0] | (static_cast<uint32_t>(p[1]) << 8) | (static_cast<uint32_t>(p[2]) << 16);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) c[q] = ((v >> (6 * q)) & 7u) | (((v >> (6 * q + 3)) & 7u) << 16);
+  }
+}
+
+constexpr int kMT = 8;  // activation tiles of 16 rows per pass (M <= 128)
+
+template <int BITS, bool BF16>
+__global__ __launch_bounds__(256) void dq_mfma_k(LinArgs a) {
+  __shared__ float red[4][kMT * 16][17];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
+  const int64_t m_base = static_cast<int64_t>(blockIdx.y) * kMT * 16;
+  const int mtiles = static_cast<int>(std::min<int64_t>(kMT, cdiv(a.M - m_base, 16)));
+  const int64_t ksteps = a.K / 32;
+  const int64_t per = cdiv(ksteps, 4);
+  const int64_t ks0 = wave * per, ks1 = std::min<int64_t>(ksteps, ks0 + per);
+
+  const int64_t nrow = std::min<int64_t>(n0 + (lane & 15), a.N - 1);
+  const uint8_t* wrow = a.packed + nrow * a.pitch;
+  const int koff = 8 * (lane >> 4);
+
+  f32x4 tot[kMT], acc[kMT];
+  float xs_acc[kMT];
+#pragma unroll
+  for (int t = 0; t < kMT; ++t) {
+    tot[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    xs_acc[t] = 0.0f;
+  }
+  const float magic_fix = BF16 ? 128.0f : 0.0f;
+  int64_t g_cur = ks0 < ks1 ? (ks0 * 32) / a.gs : 0;
+
+  auto fold = [&](int64_t g) {
+    float s[4], z[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int64_t n = std::min<int64_t>(n0 + 4 * (lane >> 4) + v, a.N - 1);
+      s[v] = load_elem(a.scales, n * a.ngroups + g, a.sz_dtype);
+      z[v] = load_elem(a.zeros, n * a.ngroups + g, a.sz_dtype) + magic_fix;
+    }
+#pragma unroll
+    for (int t = 0; t < kMT; ++t) {
+      if (t < mtiles) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) tot[t][v] += s[v] * (acc[t][v] - z[v] * xs_acc[t]);
+      }
+      acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      xs_acc[t] = 0.0f;
+    }
+  };
+
+  for (int64_t ks = ks0; ks < ks1; ++ks) {
+    const int64_t k0 = ks * 32;
+    const int64_t g = k0 / a.gs;
+    if (g != g_cur) {
+      fold(g_cur);
+      g_cur = g;
+    }
+    uint32_t c[4];
+    load8<BITS>(wrow, k0 + koff, c);
+    u32x4 af;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      if constexpr (!BF16) {
+        f16x2 h = __builtin_bit_cast(f16x2, c[p] | 0x64006400u) - f16x2{1024.0f16, 1024.0f16};
+        af[p] = __builtin_bit_cast(uint32_t, h);
+      } else {
+        af[p] = c[p] | 0x43004300u;
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kMT; ++t) {
+      if (t < mtiles) {
+        const int64_t m = m_base + t * 16 + (lane & 15);
+        u32x4 bf = {0u, 0u, 0u, 0u};
+        if (m < a.M) bf = *reinterpret_cast<const u32x4*>(a.x + m * a.K + k0 + koff);
+        float xs = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          xs += BF16 ? bf16_bits_to_f32(bf[e] & 0xffffu) : f16_bits_to_f32(bf[e] & 0xffffu);
+          xs += BF16 ? bf16_bits_to_f32(bf[e] >> 16) : f16_bits_to_f32(bf[e] >> 16);
+        }
+        xs += __shfl_xor(xs, 16, 64);
+        xs += __shfl_xor(xs, 32, 64);
+        xs_acc[t] += xs;
+        if constexpr (BF16)
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af), __builtin_bit_cast(bf16x8, bf),
+                                                           acc[t], 0, 0, 0);
+        else
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, af), __builtin_bit_cast(f16x8, bf),
+                                                          acc[t], 0, 0, 0);
+      }
+    }
+  }
+  if (ks0 < ks1) fold(g_cur);
+
+  // D layout: lane l, register v -> weight row 4*(l/16) + v, activation row l%16
+#pragma unroll
+  for (int t = 0; t < kMT; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) red[wave][t * 16 + (lane & 15)][4 * (lane >> 4) + v] = tot[t][v];
+  __syncthreads();
+  for (int i = tid; i < mtiles * 16 * 16; i += 256) {
+    const int ml = i / 16, nl = i % 16;
+    const int64_t m = m_base + ml, n = n0 + nl;
+    if (m >= a.M || n >= a.N) continue;
+    float v = red[0][ml][nl] + red[1][ml][nl] + red[2][ml][nl] + red[3][ml][nl];
+    if (a.bias) v += load_elem(a.bias, n, a.bias_dtype);
+    store_elem(a.y, m * a.N + n, a.y_dtype, v);
+  }
+}
+
+// ------------------------------------------------------------- generic ----
+__device__ __forceinline__ uint32_t code_at(const uint8_t* __restrict__ row, int64_t pitch, int64_t k, int bits) {
+  if (bits == 0) return row[k];
+  const int64_t bit = k * bits;
+  const int64_t byte = bit >> 3;
+  uint32_t v = row[byte];
+  if (byte + 1 < pitch) v |= static_cast<uint32_t>(row[byte + 1]) << 8;
+  return (v >> (bit & 7)) & ((1u << bits) - 1u);
+}
+
+__global__ __launch_bounds__(256) void linear_generic(const void* __restrict__ x, int x_dtype, int64_t M,
+                                                      const uint8_t* __restrict__ packed, int bits, int64_t pitch,
+                                                      const void* __restrict__ scales, const void* __restrict__ zeros,
+                                                      int sz_dtype, const int32_t* __restrict__ g_idx, int gs,
+                                                      int64_t ngroups, const void* __restrict__ bias, int bias_dtype,
+                                                      int64_t N, int64_t K, void* __restrict__ y) {
+  const int64_t w = blockIdx.x * 4LL + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (w >= M * N) return;
+  const int64_t m = w / N, n = w - (w / N) * N;
+  const uint8_t* row = packed + n * pitch;
+  float acc = 0.0f;
+  for (int64_t k = lane; k < K; k += 64) {
+    const int64_t g = g_idx ? std::min<int64_t>(std::max<int64_t>(g_idx[k], 0), ngroups - 1) : k / gs;
+    const float q = static_cast<float>(code_at(row, pitch, k, bits));
+    const float z = load_elem(zeros, n * ngroups + g, sz_dtype);
+    const float s = load_elem(scales, n * ngroups + g, sz_dtype);
+    const float d = q - z;
+    const float wv = d * s;
+    acc += load_elem(x, m * K + k, x_dtype) * wv;
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) {
+    if (bias) acc += load_elem(bias, n, bias_dtype);
+    store_elem(y, m * N + n, x_dtype, acc);
+  }
+}
+
+template <int BITS, bool BF16>
+int launch_fast(hipStream_t st, const LinArgs& a) {
+  using F = Fmt<BITS>;
+  const int64_t nch = a.K / F::CB;
+  if (a.M <= 4) {
+    const size_t lds = static_cast<size_t>(a.M) * a.K * 2 + static_cast<size_t>(a.M) * nch * 4;
+    if (lds <= 64 * 1024) {
+      const int64_t nbatches = cdiv(a.N, kRB);
+      const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(cdiv(nbatches, 4), 2048));
+      switch (a.M) {
+        case 1: hipLaunchKernelGGL((gemv_k<BITS, BF16, 1>), dim3(blocks), dim3(256), lds, st, a); break;
+        case 2: hipLaunchKernelGGL((gemv_k<BITS, BF16, 2>), dim3(blocks), dim3(256), lds, st, a); break;
+        case 3: hipLaunchKernelGGL((gemv_k<BITS, BF16, 3>), dim3(blocks), dim3(256), lds, st, a); break;
+        default: hipLaunchKernelGGL((gemv_k<BITS, BF16, 4>), dim3(blocks), dim3(256), lds, st, a); break;
+      }
+      return check_launch("gemv");
+    }
+  }
+  const dim3 grid(static_cast<unsigned>(cdiv(a.N, 16)), static_cast<unsigned>(cdiv(a.M, kMT * 16)));
+  hipLaunchKernelGGL((dq_mfma_k<BITS, BF16>), grid, dim3(256), 0, st, a);
+  return check_launch("dq_mfma");
+}
+
+}  // namespace
+}  // namespace gptq
+
+using namespace gptq;
+
+extern "C" int gptq_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packed, int bits, const void* scales,
+                           const void* zeros, int sz_dtype, const int32_t* g_idx, int group_size, int64_t ngroups,
+                           const void* bias, int bias_dtype, int64_t N, int64_t K, void* y, gptq_stream_t stream) {
+  clear_error();
+  GPTQ_REQUIRE(x && packed && scales && zeros && y, GPTQ_ERR_ARG, "linear: null pointer");
+  GPTQ_REQUIRE(bits == 0 || bits == 2 || bits == 3 || bits == 4 || bits == 8, GPTQ_ERR_ARG, "linear: bits=%d", bits);
+  GPTQ_REQUIRE(valid_dtype(x_dtype) && valid_dtype(sz_dtype) && (!bias || valid_dtype(bias_dtype)), GPTQ_ERR_DTYPE,
+               "linear: bad dtype");
+  GPTQ_REQUIRE(M >= 0 && N > 0 && K > 0 && ngroups > 0 && (g_idx || group_size > 0), GPTQ_ERR_SHAPE,
+               "linear: bad shape");
+  GPTQ_REQUIRE(g_idx || cdiv(K, group_size) <= ngroups, GPTQ_ERR_SHAPE, "linear: too few groups");
+  if (M == 0) return GPTQ_OK;
+  hipStream_t st = as_hip(stream);
+  const int eb = bits == 0 ? 8 : bits;
+  const int64_t pitch = (K * eb + 7) / 8;
+  LinArgs a{static_cast<const uint16_t*>(x), M, packed, pitch, scales, zeros, sz_dtype, group_size, ngroups,
+            bias, bias_dtype, N, K, static_cast<uint16_t*>(y), x_dtype};
+  int cb = eb == 4 ? 32 : eb == 2 ? 64 : eb == 8 ? 16 : 128;
+  const bool fast = x_dtype != GPTQ_F32 && !g_idx && K % cb == 0 && group_size % cb == 0 && K % 32 == 0 &&
+                    (reinterpret_cast<uintptr_t>(packed) % 16) == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0;
+  if (fast) {
+    const bool bf = x_dtype == GPTQ_BF16;
+    switch (eb) {
+      case 4: return bf ? launch_fast<4, true>(st, a) : launch_fast<4, false>(st, a);
+      case 3: return bf ? launch_fast<3, true>(st, a) : launch_fast<3, false>(st, a);
+      case 2: return bf ? launch_fast<2, true>(st, a) : launch_fast<2, false>(st, a);
+      default: return bf ? launch_fast<8, true>(st, a) : launch_fast<8, false>(st, a);
+    }
+  }
+  const unsigned blocks = static_cast<unsigned>(cdiv(M * N, 4));
+  hipLaunchKernelGGL(linear_generic, dim3(blocks), dim3(256), 0, st, x, x_dtype, M, packed, bits == 0 ? 0 : bits,
+                     pitch, scales, zeros, sz_dtype, g_idx, group_size, ngroups, bias, bias_dtype, N, K, y);
+  return check_launch("linear_generic");
+}

@@ -1,0 +1,176 @@
+"""QuantizedLinear and the ``gptq::linear`` operator (models/layers.py:15-188).
+
+The reference's forward calls ``torch.ops.gptq.linear(x, qweight, scales,
+zeros, g_idx, bias)`` whenever ``torch.ops.gptq`` exists (:150-153) and
+otherwise ``F.linear(x, unpack_weights(), bias)`` (:155-157).  This module
+registers that operator, implemented by the HIP dequant-GEMV/GEMM, with the
+fallback's semantics (fp32 dequantized weights, fp32 accumulation, output in
+x's dtype).
+
+Buffers keep the reference layout: qweight uint8 (N, ceil(K/2)) for 4-bit
+(byte = w[2i] | w[2i+1] << 4) and (N, K) one code per byte otherwise
+(:49-55); fp16 scales/zeros (N, ceil(K/g)) (:56-57).  ``packed=True`` stores
+2/3-bit codes as LSB-first bit streams too (ceil(K*bits/8) bytes per row),
+the layout of the W3A16 GEMV.  ``g_idx[k]`` holds the group of input column
+k (k // group_size unless act-order reordered the groups); the reference's
+placeholder arange(K) (:60, unused by its own unpack) is recognised and read
+as contiguous groups.
+"""
+from __future__ import annotations
+
+import math
+import weakref
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from .. import _ops
+
+# ------------------------------------------------------------- operator --
+
+_OP_LIB = None
+_layout_cache: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
+
+
+def _infer_bits(qweight: torch.Tensor, K: int) -> int:
+    """Code width from the row length: K -> one code per byte (0), else the
+    packed width whose pitch ceil(K*b/8) matches (4 preferred)."""
+    pitch = qweight.shape[1]
+    if pitch == K:
+        return 0
+    for b in (4, 3, 2):
+        if pitch == (K * b + 7) // 8:
+            return b
+    raise ValueError(f"qweight rows of {pitch} bytes match no code width for in_features={K}")
+
+
+def _group_layout(g_idx: torch.Tensor, K: int, ngroups: int):
+    """(group_size, g_idx or None): contiguous groups are passed as a group
+    size (fast kernels); anything else as the g_idx gather.  The answer is
+    cached per g_idx tensor and version (one device sync the first time)."""
+    key = _layout_cache.get(g_idx)
+    if key is not None and key[0] == g_idx._version:
+        return key[1]
+    gs = math.ceil(K / ngroups)
+    ar = torch.arange(K, device=g_idx.device, dtype=torch.int32)
+    gi = g_idx.to(torch.int32)
+    if bool(torch.equal(gi, ar // gs)):
+        res = (gs, None)
+    elif ngroups != K and bool(torch.equal(gi, ar)):
+        res = (gs, None)  # the reference's placeholder arange(K)
+    else:
+        res = (gs, gi.contiguous())
+    _layout_cache[g_idx] = (g_idx._version, res)
+    return res
+
+
+def _linear_impl(x, qweight, scales, zeros, g_idx, bias):
+    K = g_idx.numel()
+    bits = _infer_bits(qweight, K)
+    gs, gi = _group_layout(g_idx, K, scales.shape[1])
+    return _ops.linear(x, qweight, bits, scales, zeros, K, g_idx=gi, group_size=gs, bias=bias)
+
+
+def register_ops():
+    """Define gptq::linear (idempotent)."""
+    global _OP_LIB
+    if _OP_LIB is not None:
+        return
+    if hasattr(torch.ops, "gptq") and hasattr(torch.ops.gptq, "linear"):
+        return
+    lib = torch.library.Library("gptq", "DEF")
+    lib.define("linear(Tensor x, Tensor qweight, Tensor scales, Tensor zeros, Tensor g_idx, Tensor? bias) -> Tensor")
+    lib.impl("linear", _linear_impl, "CUDA")
+    _OP_LIB = lib
+
+
+register_ops()
+
+
+# -------------------------------------------------------- QuantizedLinear --
+
+class QuantizedLinear(nn.Module):
+    """Quantized Linear layer (models/layers.py:15-188)."""
+
+    def __init__(self, bits: int, group_size: int, in_features: int, out_features: int, bias: bool = True,
+                 packed: bool = False):
+        super().__init__()
+        self.bits = bits
+        self.group_size = group_size if group_size > 0 else in_features
+        self.in_features = in_features
+        self.out_features = out_features
+        self.packed = packed or bits == 4
+        self.num_groups = math.ceil(in_features / self.group_size)
+        if self.packed:
+            weight_shape = (out_features, (in_features * bits + 7) // 8)
+        else:
+            weight_shape = (out_features, in_features)
+        self.register_buffer("qweight", torch.zeros(weight_shape, dtype=torch.uint8))
+        self.register_buffer("scales", torch.zeros((out_features, self.num_groups), dtype=torch.float16))
+        self.register_buffer("zeros", torch.zeros((out_features, self.num_groups), dtype=torch.float16))
+        self.register_buffer("g_idx", torch.arange(in_features, dtype=torch.int32) // self.group_size)
+        if bias:
+            self.register_parameter("bias", nn.Parameter(torch.zeros(out_features)))
+        else:
+            self.register_parameter("bias", None)
+
+    def pack_weights(self, weight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor,
+                     g_idx: Optional[torch.Tensor] = None):
+        """Store integer codes (N, K) and fp16 scales/zeros (:67-96)."""
+        codes = weight.to(torch.uint8)
+        self.qweight.data = _ops.pack(codes, self.bits) if self.packed else codes.contiguous()
+        self.scales.data = scales.to(torch.float16).reshape(self.out_features, -1).contiguous()
+        self.zeros.data = zeros.to(torch.float16).reshape(self.out_features, -1).contiguous()
+        if g_idx is not None:
+            self.g_idx.data = g_idx.to(torch.int32).to(self.qweight.device)
+
+    def unpack_weights(self) -> torch.Tensor:
+        """fp32 (N, K) = (q - zero) * scale per group (:98-138), bit-exact."""
+        bits = self.bits if self.packed else 0
+        gs, gi = _group_layout(self.g_idx, self.in_features, self.num_groups)
+        return _ops.dequant(self.qweight, bits, self.scales, self.zeros, self.in_features, g_idx=gi,
+                            group_size=gs)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """:140-157 -- the gptq::linear operator, registered above."""
+        return torch.ops.gptq.linear(x, self.qweight, self.scales, self.zeros, self.g_idx, self.bias)
+
+    @classmethod
+    def from_linear(cls, linear_layer: nn.Linear, bits: int = 4, group_size: int = 128,
+                    packed: bool = False) -> "QuantizedLinear":
+        """:159-188 (shape and bias only; codes come from pack_weights /
+        from_gptq)."""
+        q = cls(bits=bits, group_size=group_size, in_features=linear_layer.in_features,
+                out_features=linear_layer.out_features, bias=linear_layer.bias is not None, packed=packed)
+        q = q.to(linear_layer.weight.device)
+        if linear_layer.bias is not None:
+            q.bias.data = linear_layer.bias.data
+        return q
+
+    @classmethod
+    def from_gptq(cls, gptq, linear_layer: Optional[nn.Linear] = None, packed: bool = True) -> "QuantizedLinear":
+        """Build from a GPTQ object after ``fasterquant()``: codes, scales,
+        zeros and act-order g_idx."""
+        layer = linear_layer if linear_layer is not None else gptq.layer
+        gs = getattr(gptq, "_gs_used", gptq.group_size)
+        q = cls(bits=gptq.bits, group_size=gs if gs > 0 else layer.in_features, in_features=layer.in_features,
+                out_features=layer.out_features, bias=layer.bias is not None, packed=packed)
+        q = q.to(layer.weight.device)
+        q.pack_weights(gptq.qcodes, gptq.scale, gptq.zero, gptq.g_idx)
+        if layer.bias is not None:
+            q.bias.data = layer.bias.data.clone()
+        return q
+
+
+def replace_with_quantized_layers(model: nn.Module, quantizers: dict, packed: bool = True) -> nn.Module:
+    """models/layers.py:285-315: swap each quantized nn.Linear (by name) for a
+    QuantizedLinear built from its GPTQ result."""
+    for name, gptq in quantizers.items():
+        parent = model
+        parts = name.split(".")
+        for p in parts[:-1]:
+            parent = getattr(parent, p)
+        old = getattr(parent, parts[-1])
+        setattr(parent, parts[-1], QuantizedLinear.from_gptq(gptq, old, packed=packed))
+    return model

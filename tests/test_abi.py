@@ -1,0 +1,78 @@
+"""CPU checks of the C ABI: the library loads, exports exactly the entry
+points that include/gptq_hip.h declares, and the ctypes signatures cover
+them.  No compute calls (there is no GPU here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gptq_hip.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(gptq_[a-z0-9_]+)\s*\(", text))
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    assert "gptq_hessian_accumulate" in names and "gptq_linear" in names
+    assert len(names) >= 15
+
+
+def test_library_exports_every_declared_symbol():
+    from distributed_gptq_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built")
+    h = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in sorted(declared()) if not hasattr(h, n)]
+    assert not missing, missing
+
+
+def test_ctypes_signatures_match_header():
+    from distributed_gptq_amd import _lib
+    assert set(_lib.SIGNATURES) == declared()
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    for name, (_, args) in _lib.SIGNATURES.items():
+        m = re.search(name + r"\s*\(([^)]*)\)", text)
+        params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
+        assert len(params) == len(args), (name, len(params), len(args))
+
+
+def test_library_loads_and_reports_version():
+    from distributed_gptq_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built")
+    h = _lib.load()
+    assert h.gptq_abi_version() == 1
+    assert h.gptq_last_error() == b""
+    # workspace queries are host-only arithmetic
+    assert h.gptq_hessian_workspace_size(65536, 768) > 0
+    assert h.gptq_factor_workspace_size(4096) >= 4096 * 4096 * 4
+    assert h.gptq_sweep_workspace_size(4096, 4096, 128) == 4096 * 128 * 4
+
+
+def test_entry_points_reject_bad_arguments_without_gpu():
+    """Argument checks run on the host before any launch."""
+    from distributed_gptq_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built")
+    h = _lib.load()
+    null = ctypes.c_void_p(0)
+    rc = h.gptq_hessian_accumulate(null, null, 16, 8, 8, 0, null, 0, null)
+    assert rc == _lib.ERR_ARG
+    assert b"null" in h.gptq_last_error()
+    dummy = ctypes.c_void_p(16)
+    rc = h.gptq_pack(dummy, 4, 8, 5, dummy, null)
+    assert rc == _lib.ERR_ARG and b"bits" in h.gptq_last_error()
+    rc = h.gptq_pack_reference_layout(dummy, 3, 8, 4, dummy, null)
+    assert rc == _lib.ERR_SHAPE
+    rc = h.gptq_damp_factor(dummy, 8, ctypes.c_float(1.0), ctypes.c_float(0.01), null, 7, null, dummy, null, dummy,
+                            dummy, 10 ** 9, null)
+    assert rc == _lib.ERR_ARG and b"mode" in h.gptq_last_error()
+    rc = h.gptq_damp_factor(dummy, 64, ctypes.c_float(1.0), ctypes.c_float(0.01), null, 1, null, dummy, null, dummy,
+                            dummy, 16, null)
+    assert rc == _lib.ERR_WORKSPACE

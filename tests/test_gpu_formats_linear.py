@@ -1,0 +1,176 @@
+"""GPU parity of the packing formats (bit-exact), dequantisation (bit-exact
+fp32) and the dequant GEMV/GEMM behind gptq::linear (fp32 accumulation;
+outputs within the tolerance of their dtype against the fp64 oracle)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gptq_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+@pytest.mark.parametrize("N,K", [(5, 7), (16, 256), (33, 1000)])
+def test_pack_unpack_bit_exact(hip, bits, N, K):
+    from distributed_gptq_amd import _ops
+    rng = np.random.default_rng(bits * K)
+    codes = rng.integers(0, 2 ** bits, (N, K)).astype(np.uint8)
+    p = _ops.pack(torch.from_numpy(codes).cuda(), bits)
+    np.testing.assert_array_equal(p.cpu().numpy(), O.pack_bitstream(codes, bits))
+    np.testing.assert_array_equal(_ops.unpack(p, bits, K).cpu().numpy(), codes)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+def test_reference_layout_bit_exact(hip, bits):
+    from distributed_gptq_amd import _ops
+    rng = np.random.default_rng(bits)
+    codes = rng.integers(0, 2 ** bits, (64, 40)).astype(np.uint8)
+    out = _ops.pack_reference_layout(torch.from_numpy(codes).cuda(), bits).cpu().numpy()
+    np.testing.assert_array_equal(out, O.ref_pack_weights(codes, bits))
+
+
+@pytest.mark.parametrize("bits", [0, 2, 3, 4, 8])
+@pytest.mark.parametrize("sdt", [torch.float16, torch.float32])
+def test_dequant_bit_exact(hip, bits, sdt):
+    from distributed_gptq_amd import _ops
+    rng = np.random.default_rng(bits + 10)
+    N, K, gs = 24, 384, 128
+    eb = 8 if bits == 0 else bits
+    codes = rng.integers(0, 2 ** eb, (N, K)).astype(np.uint8)
+    scales = torch.from_numpy(rng.uniform(1e-3, 1e-2, (N, 3))).to(sdt)
+    zeros = torch.from_numpy(rng.integers(0, 2 ** eb, (N, 3)).astype(np.float64) + 0.25).to(sdt)
+    packed = codes if bits == 0 else O.pack_bitstream(codes, bits)
+    out = _ops.dequant(torch.from_numpy(packed).cuda(), bits, scales.cuda(), zeros.cuda(), K, group_size=gs)
+    ref = O.dequant(codes, scales.float().numpy(), zeros.float().numpy(), np.arange(K) // gs)
+    np.testing.assert_array_equal(out.cpu().numpy(), ref)
+    # the reference's own formula in torch: (w - zeros) * scales on fp32
+    w = torch.from_numpy(codes).float()
+    tref = (w - zeros.repeat_interleave(gs, 1).float()) * scales.repeat_interleave(gs, 1).float()
+    assert torch.equal(out.cpu(), tref)
+
+
+def _case(M, N, K, bits, gs, seed, xdt):
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(0, 2 ** bits, (N, K)).astype(np.uint8)
+    ng = -(-K // gs)
+    scales = torch.from_numpy(rng.uniform(1e-3, 1e-2, (N, ng))).half()
+    zeros = torch.full((N, ng), float(2 ** (bits - 1))).half()
+    x = torch.from_numpy(rng.standard_normal((M, K))).to(xdt)
+    return codes, scales, zeros, x
+
+
+TOL = {torch.float16: 3e-3, torch.bfloat16: 1.6e-2, torch.float32: 1e-5}
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+@pytest.mark.parametrize("M", [1, 3, 16, 40, 128])
+def test_linear_fast_paths(hip, xdt, bits, M):
+    from distributed_gptq_amd import _ops
+    N, K, gs = 96, 1024, 128
+    codes, scales, zeros, x = _case(M, N, K, bits, gs, M * 10 + bits, xdt)
+    bias = torch.randn(N).to(xdt)
+    packed = torch.from_numpy(O.pack_bitstream(codes, bits)).cuda()
+    y = _ops.linear(x.cuda(), packed, bits, scales.cuda(), zeros.cuda(), K, group_size=gs, bias=bias.cuda())
+    assert y.dtype == xdt and y.shape == (M, N)
+    ref = O.linear(x.float().numpy(), codes, scales.numpy(), zeros.numpy(), np.arange(K) // gs, bias.float().numpy())
+    err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err < TOL[xdt], err
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
+def test_linear_generic_path_gidx_and_fp32(hip, xdt):
+    """act-order g_idx gather and fp32 activations take the generic kernel."""
+    from distributed_gptq_amd import _ops
+    N, K, gs = 40, 200, 50
+    codes, scales, zeros, x = _case(5, N, K, 4, gs, 3, xdt)
+    g_idx = np.random.default_rng(0).permutation(np.arange(K) // gs).astype(np.int32)
+    packed = torch.from_numpy(O.pack_bitstream(codes, 4)).cuda()
+    y = _ops.linear(x.cuda(), packed, 4, scales.cuda(), zeros.cuda(), K, g_idx=torch.from_numpy(g_idx).cuda())
+    ref = O.linear(x.float().numpy(), codes, scales.numpy(), zeros.numpy(), g_idx)
+    err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err < TOL[xdt] * 10, err
+
+
+def test_quantized_linear_op(hip):
+    from distributed_gptq_amd.models.layers import QuantizedLinear
+    N, K, gs = 64, 512, 128
+    codes, scales, zeros, x = _case(2, N, K, 4, gs, 9, torch.float16)
+    ql = QuantizedLinear(4, gs, K, N, bias=True).cuda()
+    ql.pack_weights(torch.from_numpy(codes).cuda(), scales.cuda(), zeros.cuda())
+    ql.bias.data = torch.randn(N, device="cuda")
+    assert ql.qweight.shape == (N, K // 2)
+    # packed buffer is the reference's byte layout (models/layers.py:85-89)
+    np.testing.assert_array_equal(ql.qweight.cpu().numpy(), O.pack_bitstream(codes, 4))
+    Wd = ql.unpack_weights()
+    np.testing.assert_array_equal(Wd.cpu().numpy(), O.dequant(codes, scales.numpy(), zeros.numpy(),
+                                                              np.arange(K) // gs))
+    y = ql(x.cuda())
+    y2 = torch.ops.gptq.linear(x.cuda(), ql.qweight, ql.scales, ql.zeros, ql.g_idx, ql.bias)
+    assert torch.equal(y, y2)
+    ref = x.double().numpy() @ Wd.double().cpu().numpy().T + ql.bias.double().cpu().numpy()
+    err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err < TOL[torch.float16]
+    # the reference's placeholder g_idx = arange(K) means contiguous groups
+    ql.g_idx.data = torch.arange(K, dtype=torch.int32, device="cuda")
+    assert torch.equal(ql(x.cuda()), y)
+
+
+def test_quantized_linear_from_gptq_actorder(hip):
+    from distributed_gptq_amd import GPTQ
+    from distributed_gptq_amd.models.layers import QuantizedLinear
+    torch.manual_seed(2)
+    lin = torch.nn.Linear(256, 64).cuda().half()
+    X = torch.randn(2, 128, 256, device="cuda").half()
+    q = GPTQ(lin, bits=3, group_size=64, actorder=True, device="cuda")
+    q.add_batch(X)
+    q.fasterquant()
+    for packed in (True, False):
+        ql = QuantizedLinear.from_gptq(q, packed=packed)
+        Wd = ql.unpack_weights()
+        # the layer's dequantized weight (fp16) equals the stored codes' dequant
+        np.testing.assert_allclose(Wd.half().cpu().numpy(), lin.weight.data.cpu().numpy(), rtol=0, atol=0)
+        y = ql(X[0])
+        ref = X[0].double().cpu().numpy() @ Wd.double().cpu().numpy().T + lin.bias.double().cpu().numpy()
+        err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+        assert err < TOL[torch.float16]
+
+
+def test_tensor_quantize_dequantize(hip):
+    from distributed_gptq_amd import kernels
+    assert kernels.check_triton_availability()
+    x = torch.randn(10, 100)
+    q, s, z = kernels.quantize_tensor(x, bits=4, group_size=128)
+    xn = x.numpy().reshape(-1)
+    for g in range(len(s)):
+        seg = xn[g * 128:(g + 1) * 128]
+        sg = np.float32((seg.max() - seg.min()) / np.float32(15))
+        zg = np.float32(-seg.min() / sg)
+        assert s[g].item() == pytest.approx(float(sg), rel=1e-6)
+        assert z[g].item() == pytest.approx(float(zg), rel=1e-5, abs=1e-6)
+        v = seg / sg + zg
+        expect = np.clip(np.floor(np.abs(v) + 0.5) * np.sign(v), 0, 15)  # half away from zero
+        np.testing.assert_array_equal(q.cpu().numpy().reshape(-1)[g * 128:(g + 1) * 128], expect)
+    d = kernels.dequantize_tensor(q, s, z, 128).cpu()
+    gi = np.arange(1000) // 128
+    ref = (q.cpu().numpy().reshape(-1).astype(np.float32) - z.cpu().numpy()[gi]) * s.cpu().numpy()[gi]
+    np.testing.assert_array_equal(d.numpy().reshape(-1), ref)
+
+
+def test_triton_quantized_linear(hip):
+    from distributed_gptq_amd import kernels
+    tl = kernels.TritonQuantizedLinear(256, 32, bits=4, group_size=64)
+    w = torch.randn(32, 256) * 0.02
+    tl.quantize_weights(w)
+    x = torch.randn(3, 256, device="cuda", dtype=torch.float16)
+    y = tl.forward(x)
+    s = tl.scales.float().cpu().numpy()
+    z = tl.zeros.float().cpu().numpy()
+    codes = tl.qweight.cpu().numpy().view(np.uint8)
+    ref = O.linear(x.float().cpu().numpy(), codes, s, z, np.arange(256) // 64)
+    err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err < 3e-3
+    # dequantized weights are close to the originals
+    Wd = O.dequant(codes, s, z, np.arange(256) // 64)
+    assert np.abs(Wd - w.numpy()).max() < 0.02 * 8 / 15 + 1e-3

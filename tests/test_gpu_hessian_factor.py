@@ -1,0 +1,121 @@
+"""GPU parity: Hessian accumulation (H within 1e-5 relative Frobenius error of
+the fp64 Gram matrix of the same inputs) and the damped inverse factors."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gptq_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(a, b):
+    return float(np.linalg.norm(np.asarray(a, np.float64) - b) / np.linalg.norm(b))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("n,K", [(1, 8), (77, 10), (2048, 256), (4096, 1000), (5000, 768)])
+def test_hessian_matches_fp64(hip, dtype, n, K):
+    from distributed_gptq_amd import _ops
+    g = torch.Generator(device="cpu").manual_seed(n * 7 + K)
+    X = torch.randn(n, K, generator=g)
+    X[:, :3] *= 20
+    Xd = X.to(dtype).cuda()
+    H = torch.zeros(K, K, device="cuda")
+    _ops.hessian_accumulate(H, Xd)
+    Hn = H.cpu().numpy()
+    Href = Xd.double().cpu().numpy()
+    Href = Href.T @ Href
+    assert _rel(Hn, Href) < 1e-5
+    assert np.array_equal(Hn, Hn.T), "H must be exactly symmetric"
+
+
+def test_hessian_accumulates_and_nonaligned_rows(hip):
+    from distributed_gptq_amd import _ops
+    K = 520
+    X = torch.randn(3, 333, K + 3, device="cuda", dtype=torch.bfloat16)[..., :K]  # strided rows
+    H = torch.zeros(K, K, device="cuda")
+    for i in range(3):
+        _ops.hessian_accumulate(H, X[i])
+    Xn = X.double().cpu().numpy().reshape(-1, K)
+    assert _rel(H.cpu().numpy(), Xn.T @ Xn) < 1e-5
+
+
+def test_hessian_c1_config(hip):
+    """Config 1: Linear 768, 128 x 512 fp32 tokens, 8 outlier channels x20."""
+    from distributed_gptq_amd import GPTQ
+    g = torch.Generator().manual_seed(0)
+    lin = torch.nn.Linear(768, 768)
+    with torch.no_grad():
+        lin.weight.normal_(0, 0.02, generator=g)
+    X = torch.randn(128, 512, 768, generator=g)
+    idx = torch.randperm(768, generator=g)[:8]
+    X[..., idx] *= 20
+    q = GPTQ(lin.cuda(), bits=4, group_size=128, device="cuda")
+    for i in range(128):
+        q.add_batch(X[i:i + 1].cuda())
+    assert q.nsamples == 128
+    Xn = X.double().numpy().reshape(-1, 768)
+    assert _rel(q.H.cpu().numpy(), Xn.T @ Xn) < 1e-5
+
+
+def _spd_H(K, seed, n=None):
+    rng = np.random.default_rng(seed)
+    n = n or 4 * K
+    X = rng.standard_normal((n, K)).astype(np.float32)
+    X[:, rng.integers(0, K, 4)] *= 20
+    return (X.astype(np.float64).T @ X.astype(np.float64)).astype(np.float32)
+
+
+@pytest.mark.parametrize("K", [37, 64, 200, 1024])
+def test_factor_upper_chol_inverse(hip, K):
+    from distributed_gptq_amd import _lib, _ops
+    H = _spd_H(K, K)
+    ns = 8
+    U, _, dead, info = _ops.damp_factor(torch.from_numpy(H).cuda(), 2.0 / ns, 0.01, None,
+                                        _lib.FACTOR_UPPER_CHOL_INV, want_dead=True)
+    assert int(info.item()) == 0
+    assert int(dead.sum().item()) == 0
+    Hd, _ = O.prepare_canonical_H(H.astype(np.float64), ns, 0.01)
+    Ur = O.upper_chol_of_inverse(Hd)
+    Un = U.cpu().numpy()
+    assert np.all(np.tril(Un, -1) == 0)
+    assert _rel(Un, Ur) < 2e-4
+
+
+@pytest.mark.parametrize("K", [50, 256, 700])
+def test_factor_full_inverse(hip, K):
+    from distributed_gptq_amd import _lib, _ops
+    H = _spd_H(K, K + 1)
+    Hinv, Hd, _, info = _ops.damp_factor(torch.from_numpy(H).cuda(), 1.0 / 16, 0.01, None,
+                                         _lib.FACTOR_FULL_INVERSE, want_hd=True)
+    assert int(info.item()) == 0
+    Hdr = O.damp_ref(H.astype(np.float64), 16, 0.01)
+    assert _rel(Hd.cpu().numpy(), Hdr) < 1e-6
+    assert _rel(Hinv.cpu().numpy(), O.full_inverse(Hdr)) < 2e-4
+
+
+def test_factor_perm_and_dead_columns(hip):
+    from distributed_gptq_amd import _lib, _ops
+    K = 96
+    H = _spd_H(K, 5)
+    H[7, :] = 0
+    H[:, 7] = 0
+    perm = np.random.default_rng(1).permutation(K)
+    U, _, dead, info = _ops.damp_factor(torch.from_numpy(H).cuda(), 2.0 / 4, 0.01,
+                                        torch.from_numpy(perm).cuda(), _lib.FACTOR_UPPER_CHOL_INV, want_dead=True)
+    assert int(info.item()) == 0
+    d = dead.cpu().numpy()
+    assert d[7] == 1 and d.sum() == 1
+    Hd, _ = O.prepare_canonical_H(H.astype(np.float64), 4, 0.0)
+    Hp = Hd[perm][:, perm]
+    Hp[np.diag_indices(K)] += 0.01 * np.mean(np.diag(Hp))
+    assert _rel(U.cpu().numpy(), O.upper_chol_of_inverse(Hp)) < 2e-4
+
+
+def test_factor_reports_not_positive_definite(hip):
+    from distributed_gptq_amd import _lib, _ops
+    K = 80
+    H = -np.eye(K, dtype=np.float32)
+    _, _, _, info = _ops.damp_factor(torch.from_numpy(H).cuda(), 1.0, 0.0, None, _lib.FACTOR_FULL_INVERSE)
+    assert int(info.item()) > 0
