@@ -1,0 +1,335 @@
+#!/usr/bin/env python
+"""Benchmark of the GPTQ hot path on one MI355X.
+
+Workload (config 3): quantize one Llama-3-8B-shaped decoder block (hidden
+4096, 32 query / 8 KV heads of 128, SwiGLU FFN 14336, bf16 random init) to
+4-bit g128 with act-order, from 128 x 2048 calibration tokens.  A step =
+block forward over all tokens collecting the four distinct layer inputs
+(q/k/v, o, gate/up, down), four one-triangle Hessians, four damped
+Cholesky/inverse factorisations, seven column sweeps with lazy-batch
+updates, and packing of all seven layers.  Inputs (calibration activations
+and weights) are resident in HBM before timing starts.
+
+The JSON line also reports the Hessian kernel against the bf16 MFMA
+roofline, the W4A16 / W3A16 dequant-GEMV microbench (M = 1, rotating >= 1 GiB
+of distinct weight buffers so HBM, not the 256 MB last-level cache, is
+measured) and a CPU baseline: the CPU oracle timed on a bounded sample on
+this host's cores and extrapolated to one block.
+
+    python bench.py [--steps 3] [--warmup 1] [--no-cpu] [--no-gemv]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "s per 8B-shaped block quantized; Hessian MFMA TFLOP/s; W4A16 GEMV HBM GB/s"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+HID, NQ, NKV, HD, FFN = 4096, 32, 8, 128, 14336
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------ the block --
+
+class Block:
+    """Random-init Llama-3-8B-shaped decoder block (bf16)."""
+
+    def __init__(self, torch, dev, seed=2):
+        g = torch.Generator(device=dev).manual_seed(seed)
+
+        def w(n, k):
+            return (torch.randn(n, k, generator=g, device=dev, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+
+        self.w = {"q_proj": w(NQ * HD, HID), "k_proj": w(NKV * HD, HID), "v_proj": w(NKV * HD, HID),
+                  "o_proj": w(HID, NQ * HD), "gate_proj": w(FFN, HID), "up_proj": w(FFN, HID),
+                  "down_proj": w(HID, FFN)}
+        gamma = torch.ones(HID, device=dev, dtype=torch.float32)
+        idx = torch.randperm(HID, generator=g, device=dev)[:8]
+        gamma[idx] = 20.0
+        self.g1 = gamma.to(torch.bfloat16)
+        self.g2 = torch.ones(HID, device=dev, dtype=torch.bfloat16)
+        self.hkey = {"q_proj": "qkv", "k_proj": "qkv", "v_proj": "qkv", "o_proj": "o", "gate_proj": "up",
+                     "up_proj": "up", "down_proj": "down"}
+
+    @staticmethod
+    def rmsnorm(torch, x, gamma, eps=1e-5):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype) * gamma
+
+    def rope(self, torch, T, dev):
+        inv = 1.0 / (500000.0 ** (torch.arange(0, HD, 2, device=dev, dtype=torch.float32) / HD))
+        t = torch.arange(T, device=dev, dtype=torch.float32)
+        f = torch.outer(t, inv)
+        emb = torch.cat([f, f], dim=-1)
+        return emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+
+    @staticmethod
+    def apply_rope(torch, x, cos, sin):
+        x1, x2 = x[..., : HD // 2], x[..., HD // 2:]
+        return x * cos + torch.cat([-x2, x1], dim=-1) * sin
+
+    def collect(self, torch, F, z, bufs, chunk, cos, sin):
+        """Forward over all sequences; store the four layer inputs."""
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        nseq, T, _ = z.shape
+        for s0 in range(0, nseq, chunk):
+            zc = z[s0:s0 + chunk]
+            b = zc.shape[0]
+            r0, r1 = s0 * T, (s0 + b) * T
+            x1 = self.rmsnorm(torch, zc, self.g1)
+            bufs["qkv"][r0:r1].view(b, T, HID).copy_(x1)
+            q = F.linear(x1, self.w["q_proj"]).view(b, T, NQ, HD)
+            k = F.linear(x1, self.w["k_proj"]).view(b, T, NKV, HD)
+            v = F.linear(x1, self.w["v_proj"]).view(b, T, NKV, HD)
+            q = self.apply_rope(torch, q, cos[:, None], sin[:, None]).transpose(1, 2).contiguous()
+            k = self.apply_rope(torch, k, cos[:, None], sin[:, None]).transpose(1, 2)
+            k = k.repeat_interleave(NQ // NKV, dim=1).contiguous()
+            v = v.transpose(1, 2).repeat_interleave(NQ // NKV, dim=1).contiguous()
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                a = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+            a = a.transpose(1, 2).reshape(b, T, HID)
+            bufs["o"][r0:r1].view(b, T, HID).copy_(a)
+            h = zc + F.linear(a, self.w["o_proj"])
+            x2 = self.rmsnorm(torch, h, self.g2)
+            bufs["up"][r0:r1].view(b, T, HID).copy_(x2)
+            act = F.silu(F.linear(x2, self.w["gate_proj"])) * F.linear(x2, self.w["up_proj"])
+            bufs["down"][r0:r1].view(b, T, FFN).copy_(act)
+
+
+def hessian_flops(n, K):
+    """one triangle incl. the diagonal, 2 flops per multiply-add"""
+    return n * K * (K + 1)
+
+
+def run_block(args, torch, F, dev):
+    from distributed_gptq_amd import _ops, pipeline
+    blk = Block(torch, dev)
+    T, nseq = args.seqlen, args.nseq
+    n = nseq * T
+    g = torch.Generator(device=dev).manual_seed(2)
+    z = torch.randn(nseq, T, HID, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    bufs = {k: torch.empty(n, HID if k != "down" else FFN, device=dev, dtype=torch.bfloat16)
+            for k in ("qkv", "o", "up", "down")}
+    Hs = {k: torch.empty(v.shape[1], v.shape[1], device=dev, dtype=torch.float32) for k, v in bufs.items()}
+    cos, sin = blk.rope(torch, T, dev)
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+
+    def step(record):
+        e = [ev() for _ in range(4)]
+        he = {k: (ev(), ev()) for k in Hs}
+        e[0].record()
+        blk.collect(torch, F, z, bufs, args.chunk, cos, sin)
+        e[1].record()
+        for k, X in bufs.items():
+            Hs[k].zero_()
+            he[k][0].record()
+            _ops.hessian_accumulate(Hs[k], X)
+            he[k][1].record()
+        e[2].record()
+        res = pipeline.quantize_layers(blk.w, blk.hkey, {k: (Hs[k], nseq) for k in Hs}, bits=args.bits,
+                                       group_size=128, blocksize=128, percdamp=0.01, actorder=True,
+                                       want_dequant=True, check=True)
+        e[3].record()
+        if record is not None:
+            torch.cuda.synchronize()
+            record.append({
+                "forward_ms": e[0].elapsed_time(e[1]),
+                "hessian_ms": e[1].elapsed_time(e[2]),
+                "quantize_ms": e[2].elapsed_time(e[3]),
+                "hessian_kernel_ms": {k: he[k][0].elapsed_time(he[k][1]) for k in he},
+            })
+        return res
+
+    for _ in range(args.warmup):
+        step(None)
+    torch.cuda.synchronize()
+    recs = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        res = step(recs)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    s_per_block = wall / args.steps
+    hflops = sum(hessian_flops(n, X.shape[1]) for X in bufs.values())
+    hms = sum(sum(r["hessian_kernel_ms"].values()) for r in recs) / len(recs)
+    per_kernel = {k: sum(r["hessian_kernel_ms"][k] for r in recs) / len(recs) for k in Hs}
+    breakdown = {k: round(sum(r[k] for r in recs) / len(recs), 3) for k in ("forward_ms", "hessian_ms", "quantize_ms")}
+    losses = {k: float(v.losses_sum.item()) for k, v in res.items()}
+    del bufs, Hs, z
+    torch.cuda.empty_cache()
+    return dict(s_per_block=s_per_block, wall=wall, hessian_flops=hflops, hessian_ms=hms,
+                hessian_kernel_ms=per_kernel, breakdown=breakdown, tokens=n, losses=losses)
+
+
+# ------------------------------------------------------------ GEMV bench --
+
+GEMV_SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336), (28672, 4096)]
+
+
+def gemv_bytes(N, K, bits, M=1):
+    return N * K * bits // 8 + N * (K // 128) * 4 + M * K * 2 + M * N * 2
+
+
+def run_gemv(args, torch, dev, bits, M=1, min_bytes=1 << 30, reps=3):
+    from distributed_gptq_amd import _ops
+    out = {}
+    g = torch.Generator(device=dev).manual_seed(3)
+    for (N, K) in GEMV_SHAPES:
+        nbytes = gemv_bytes(N, K, bits, M)
+        R = max(2, math.ceil(min_bytes / (N * K * bits // 8)))
+        codes = torch.randint(0, 2 ** bits, (N, K), generator=g, device=dev, dtype=torch.uint8)
+        q0 = _ops.pack(codes, bits)
+        qs = [q0.clone() for _ in range(R)]
+        sc = [(torch.rand(N, K // 128, generator=g, device=dev) * 9e-3 + 1e-3).half() for _ in range(R)]
+        zr = torch.full((N, K // 128), float(2 ** (bits - 1)), device=dev, dtype=torch.float16)
+        x = torch.randn(M, K, generator=g, device=dev, dtype=torch.float32).half()
+        y = torch.empty(M, N, device=dev, dtype=torch.float16)
+        for r in range(R):
+            _ops.linear(x, qs[r], bits, sc[r], zr, K, group_size=128, out=y)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(graph, stream=s):
+                for r in range(R):
+                    _ops.linear(x, qs[r], bits, sc[r], zr, K, group_size=128, out=y)
+        torch.cuda.current_stream().wait_stream(s)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * R)
+        out[f"{N}x{K}"] = {"us": round(us, 3), "GBps": round(nbytes / us * 1e-3, 1), "bytes": nbytes, "buffers": R}
+        del qs, sc, graph
+        torch.cuda.empty_cache()
+    tot_b = sum(v["bytes"] for v in out.values())
+    tot_us = sum(v["us"] for v in out.values())
+    return out, tot_b / tot_us * 1e-3
+
+
+# ------------------------------------------------------------ CPU baseline --
+
+def cpu_baseline(seconds_hint=20.0):
+    """The CPU oracle (numpy, this host's BLAS threads) on a bounded sample of
+    the block, extrapolated to one block the way the reference computes it:
+    one full-square fp32 Hessian per Linear over 128 x 2048 tokens, a fp32
+    Cholesky inverse per Linear, and the column sweep per Linear."""
+    import numpy as np
+    from threadpoolctl import threadpool_info
+    from oracle import gptq_oracle as O
+    threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    rng = np.random.default_rng(0)
+    K = 4096
+    # (a) Hessian: 2 sequences of 2048 tokens at K = 4096, fp32
+    x = rng.standard_normal((2, 2048, K), dtype=np.float32)
+    t = time.perf_counter()
+    O.add_batch(None, 0, x, dtype=np.float32)
+    t_h = (time.perf_counter() - t) / 2  # per sequence
+    # (b) damped inverse at K = 4096, fp32 (LAPACK)
+    H = (x.reshape(-1, K).T @ x.reshape(-1, K)).astype(np.float32) / 2
+    t = time.perf_counter()
+    O.upper_chol_of_inverse(O.damp_ref(H, 1, 0.01).astype(np.float32))
+    t_f = time.perf_counter() - t
+    # (c) sweep: canonical oracle on a 4096 x 1024 slice (fp32)
+    W = (rng.standard_normal((4096, 1024)) * 0.02).astype(np.float32)
+    Hs = H[:1024, :1024].astype(np.float32)
+    t = time.perf_counter()
+    O.gptq_canonical(W, Hs, 1, 4, 128, 128, 0.01, actorder=True, dtype=np.float32)
+    t_s = time.perf_counter() - t
+    sample = time.perf_counter()
+    layers = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336, 4096), (14336, 4096), (4096, 14336)]
+    hess = sum(128 * t_h * (k / K) ** 2 for _, k in layers)
+    fac = sum(t_f * (k / K) ** 3 for _, k in layers)
+    swp = sum(t_s * (n / 4096) * (k / 1024) ** 2 for n, k in layers)
+    total = hess + fac + swp
+    return {"value": round(total, 2), "unit": "s/block", "cores": threads, "kind": "port",
+            "sample": ("oracle/gptq_oracle.py in numpy fp32 on 2 x 2048 tokens (Hessian, K=4096), one damped "
+                       "Cholesky inverse at K=4096, one act-order sweep of 4096 x 1024; extrapolated per Linear "
+                       "of the block (Hessian x 128 sequences x (K/4096)^2, inverse x (K/4096)^3, sweep x "
+                       "N/4096 x (K/1024)^2) as the reference computes it (one full H per Linear)"),
+            "parts_s": {"hessian": round(hess, 2), "factor": round(fac, 2), "sweep": round(swp, 2)},
+            "sample_s": {"hessian_per_seq": round(t_h, 4), "factor_4096": round(t_f, 3),
+                         "sweep_4096x1024": round(t_s, 3)}}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--bits", type=int, default=4)
+    ap.add_argument("--nseq", type=int, default=128)
+    ap.add_argument("--seqlen", type=int, default=2048)
+    ap.add_argument("--chunk", type=int, default=8, help="sequences per forward chunk")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-gemv", action="store_true")
+    ap.add_argument("--no-block", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build quantizes on a single MI355X "
+              "(no collectives or sharded path); run it with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import torch.nn.functional as F
+    dev = torch.device("cuda", 0)
+    import distributed_gptq_amd  # noqa: F401
+    from distributed_gptq_amd import _lib
+    _lib.load()
+    result = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+              "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+              "data": "synthetic (random-init weights, N(0,1) calibration with RMSNorm outlier channels)",
+              "config": {"workload": f"llama3-8b-block-w{args.bits}g128-actorder", "hidden": HID, "heads": NQ,
+                         "kv_heads": NKV, "ffn": FFN, "tokens": args.nseq * args.seqlen, "bits": args.bits,
+                         "group_size": 128, "blocksize": 128, "percdamp": 0.01, "actorder": True,
+                         "parallelism": "single-gpu"}}
+    if not args.no_block:
+        log(f"[bench] block: {args.nseq} x {args.seqlen} tokens, warmup {args.warmup}, steps {args.steps}")
+        b = run_block(args, torch, F, dev)
+        tflops = b["hessian_flops"] / (b["hessian_ms"] * 1e-3) / 1e12
+        result.update({"value": round(b["s_per_block"], 4), "unit": "s/block",
+                       "ms_per_step": round(b["s_per_block"] * 1e3, 2),
+                       "hessian_tflops": round(tflops, 1), "breakdown_ms": b["breakdown"],
+                       "hessian_kernel_ms": {k: round(v, 3) for k, v in b["hessian_kernel_ms"].items()},
+                       "layer_losses": {k: round(v, 4) for k, v in b["losses"].items()}})
+        result["roofline"] = {"bound": "mfma", "kernel": "hessian (tile + reduce)", "achieved": round(tflops, 1),
+                              "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                              "traffic": None,
+                              "work": "n*K*(K+1) flops per Hessian, n = 262144 tokens, K in {4096 x3, 14336}"}
+        log(f"[bench] block done: {b['s_per_block']:.3f} s/block, Hessian {tflops:.1f} TFLOP/s, {b['breakdown']}")
+    if not args.no_gemv:
+        g4, agg4 = run_gemv(args, torch, dev, 4)
+        log(f"[bench] W4A16 GEMV: {g4}")
+        g3, agg3 = run_gemv(args, torch, dev, 3)
+        log(f"[bench] W3A16 GEMV: {g3}")
+        result["w4a16_gemv_gbps"] = round(agg4, 1)
+        result["w3a16_gemv_gbps"] = round(agg3, 1)
+        result["gemv"] = {"w4a16_m1": g4, "w3a16_m1": g3, "peak_GBps": PEAK_HBM_GBS,
+                          "w4a16_frac": round(agg4 / PEAK_HBM_GBS, 4)}
+    if args.no_block:
+        result.setdefault("value", None)
+    if not args.no_cpu:
+        log("[bench] CPU baseline (oracle on host cores)")
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

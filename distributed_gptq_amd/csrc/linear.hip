@@ -74,9 +74,25 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// dot of the chunk's decoded codes with x pairs; returns sum x*(code + bias)
-// where bias = 0 (fp16: exact packed subtraction of the 1024 magic) or 128
-// (bf16: the magic is left in and corrected by the caller).
+// bf16 codes carry a magic offset of 128 (0x4300 | code is 128 + code for
+// code < 128); 8-bit codes do not fit under it and are converted exactly.
+template <int BITS, bool BF16>
+struct Magic {
+  static constexpr bool kBF16Offset = BF16 && BITS != 8;
+  static constexpr float kOffset = kBF16Offset ? 128.0f : 0.0f;
+};
+
+// two small integers (lo, hi halves of c) -> the pair of bf16 values, exact
+__device__ __forceinline__ uint32_t bf16_pair_exact(uint32_t c) {
+  const uint32_t lo = __float_as_uint(static_cast<float>(c & 0xffffu));
+  const uint32_t hi = __float_as_uint(static_cast<float>(c >> 16));
+  return (lo >> 16) | (hi & 0xffff0000u);
+}
+
+// dot of the chunk's decoded codes with x pairs; returns sum x*(code + off)
+// where off = Magic::kOffset (fp16: the 1024 magic is subtracted exactly with
+// a packed fp16 op; bf16: the 128 magic is left in and corrected by the
+// caller through the x sums).
 template <int BITS, bool BF16, int P>
 __device__ __forceinline__ float chunk_dot_pair(const uint32_t* dw, uint32_t xpair, float acc) {
   const uint32_t c = decode_pair<BITS, P>(dw);
@@ -85,7 +101,7 @@ __device__ __forceinline__ float chunk_dot_pair(const uint32_t* dw, uint32_t xpa
     f16x2 h = __builtin_bit_cast(f16x2, t) - f16x2{1024.0f16, 1024.0f16};
     return __builtin_amdgcn_fdot2(h, __builtin_bit_cast(f16x2, xpair), acc, false);
   } else {
-    const uint32_t t = c | 0x43004300u;                 // 128 + code, bf16
+    const uint32_t t = Magic<BITS, BF16>::kBF16Offset ? (c | 0x43004300u) : bf16_pair_exact(c);
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, t), __builtin_bit_cast(bf16x2, xpair), acc,
                                            false);
   }
@@ -176,7 +192,7 @@ __global__ __launch_bounds__(256) void gemv_k(LinArgs a) {
         const int64_t n = std::min<int64_t>(n0 + r, a.N - 1);
         sc[r] = load_elem(a.scales, n * a.ngroups + g, a.sz_dtype);
         zc[r] = load_elem(a.zeros, n * a.ngroups + g, a.sz_dtype);
-        if constexpr (BF16) zc[r] += 128.0f;
+        zc[r] += Magic<BITS, BF16>::kOffset;
       }
 #pragma unroll
       for (int m = 0; m < MV; ++m) {
@@ -272,7 +288,7 @@ __global__ __launch_bounds__(256) void dq_mfma_k(LinArgs a) {
     acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     xs_acc[t] = 0.0f;
   }
-  const float magic_fix = BF16 ? 128.0f : 0.0f;
+  const float magic_fix = Magic<BITS, BF16>::kOffset;
   int64_t g_cur = ks0 < ks1 ? (ks0 * 32) / a.gs : 0;
 
   auto fold = [&](int64_t g) {
@@ -310,7 +326,7 @@ __global__ __launch_bounds__(256) void dq_mfma_k(LinArgs a) {
         f16x2 h = __builtin_bit_cast(f16x2, c[p] | 0x64006400u) - f16x2{1024.0f16, 1024.0f16};
         af[p] = __builtin_bit_cast(uint32_t, h);
       } else {
-        af[p] = c[p] | 0x43004300u;
+        af[p] = Magic<BITS, BF16>::kBF16Offset ? (c[p] | 0x43004300u) : bf16_pair_exact(c[p]);
       }
     }
 #pragma unroll

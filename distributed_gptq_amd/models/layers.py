@@ -30,7 +30,9 @@ from .. import _ops
 # ------------------------------------------------------------- operator --
 
 _OP_LIB = None
-_layout_cache: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
+# id(g_idx) -> (weakref to g_idx, (version, data_ptr), result); tensors
+# cannot be dict keys by value (their == is elementwise)
+_layout_cache: dict = {}
 
 
 def _infer_bits(qweight: torch.Tensor, K: int) -> int:
@@ -49,9 +51,10 @@ def _group_layout(g_idx: torch.Tensor, K: int, ngroups: int):
     """(group_size, g_idx or None): contiguous groups are passed as a group
     size (fast kernels); anything else as the g_idx gather.  The answer is
     cached per g_idx tensor and version (one device sync the first time)."""
-    key = _layout_cache.get(g_idx)
-    if key is not None and key[0] == g_idx._version:
-        return key[1]
+    hit = _layout_cache.get(id(g_idx))
+    stamp = (g_idx._version, g_idx.data_ptr())
+    if hit is not None and hit[0]() is g_idx and hit[1] == stamp:
+        return hit[2]
     gs = math.ceil(K / ngroups)
     ar = torch.arange(K, device=g_idx.device, dtype=torch.int32)
     gi = g_idx.to(torch.int32)
@@ -61,7 +64,8 @@ def _group_layout(g_idx: torch.Tensor, K: int, ngroups: int):
         res = (gs, None)  # the reference's placeholder arange(K)
     else:
         res = (gs, gi.contiguous())
-    _layout_cache[g_idx] = (g_idx._version, res)
+    key = id(g_idx)
+    _layout_cache[key] = (weakref.ref(g_idx, lambda _r, k=key: _layout_cache.pop(k, None)), stamp, res)
     return res
 
 
@@ -72,8 +76,30 @@ def _linear_impl(x, qweight, scales, zeros, g_idx, bias):
     return _ops.linear(x, qweight, bits, scales, zeros, K, g_idx=gi, group_size=gs, bias=bias)
 
 
+def _linear_setup(ctx, inputs, output):
+    x, qweight, scales, zeros, g_idx, bias = inputs
+    ctx.save_for_backward(qweight, scales, zeros, g_idx)
+    ctx.x_dtype = x.dtype
+    ctx.has_bias = bias is not None
+
+
+def _linear_backward(ctx, grad):
+    """Gradients of the fallback F.linear(x, unpack_weights(), bias): the
+    quantized weights are constants; x and bias get their usual gradients."""
+    qweight, scales, zeros, g_idx = ctx.saved_tensors
+    gx = gb = None
+    if ctx.needs_input_grad[0]:
+        K = g_idx.numel()
+        gs, gi = _group_layout(g_idx, K, scales.shape[1])
+        W = _ops.dequant(qweight, _infer_bits(qweight, K), scales, zeros, K, g_idx=gi, group_size=gs)
+        gx = (grad.float() @ W).to(ctx.x_dtype)
+    if ctx.has_bias and ctx.needs_input_grad[5]:
+        gb = grad.reshape(-1, grad.shape[-1]).float().sum(0)
+    return gx, None, None, None, None, gb
+
+
 def register_ops():
-    """Define gptq::linear (idempotent)."""
+    """Define gptq::linear with its CUDA kernel and autograd (idempotent)."""
     global _OP_LIB
     if _OP_LIB is not None:
         return
@@ -82,6 +108,7 @@ def register_ops():
     lib = torch.library.Library("gptq", "DEF")
     lib.define("linear(Tensor x, Tensor qweight, Tensor scales, Tensor zeros, Tensor g_idx, Tensor? bias) -> Tensor")
     lib.impl("linear", _linear_impl, "CUDA")
+    torch.library.register_autograd("gptq::linear", _linear_backward, setup_context=_linear_setup, lib=lib)
     _OP_LIB = lib
 
 

@@ -106,15 +106,24 @@ def test_quantized_linear_op(hip):
     Wd = ql.unpack_weights()
     np.testing.assert_array_equal(Wd.cpu().numpy(), O.dequant(codes, scales.numpy(), zeros.numpy(),
                                                               np.arange(K) // gs))
-    y = ql(x.cuda())
-    y2 = torch.ops.gptq.linear(x.cuda(), ql.qweight, ql.scales, ql.zeros, ql.g_idx, ql.bias)
+    with torch.no_grad():
+        y = ql(x.cuda())
+        y2 = torch.ops.gptq.linear(x.cuda(), ql.qweight, ql.scales, ql.zeros, ql.g_idx, ql.bias)
     assert torch.equal(y, y2)
     ref = x.double().numpy() @ Wd.double().cpu().numpy().T + ql.bias.double().cpu().numpy()
     err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
     assert err < TOL[torch.float16]
     # the reference's placeholder g_idx = arange(K) means contiguous groups
     ql.g_idx.data = torch.arange(K, dtype=torch.int32, device="cuda")
-    assert torch.equal(ql(x.cuda()), y)
+    with torch.no_grad():
+        assert torch.equal(ql(x.cuda()), y)
+    # gradients of F.linear(x, W, b) with the dequantized weight
+    xg = x.cuda().float().requires_grad_(True)
+    ql.g_idx.data = torch.arange(K, dtype=torch.int32, device="cuda") // gs
+    out = ql(xg)
+    out.backward(torch.ones_like(out))
+    np.testing.assert_allclose(xg.grad.cpu().numpy(), np.tile(Wd.sum(0).cpu().numpy(), (2, 1)), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(ql.bias.grad.cpu().numpy(), np.full(N, 2.0))
 
 
 def test_quantized_linear_from_gptq_actorder(hip):
@@ -129,9 +138,14 @@ def test_quantized_linear_from_gptq_actorder(hip):
     for packed in (True, False):
         ql = QuantizedLinear.from_gptq(q, packed=packed)
         Wd = ql.unpack_weights()
-        # the layer's dequantized weight (fp16) equals the stored codes' dequant
-        np.testing.assert_allclose(Wd.half().cpu().numpy(), lin.weight.data.cpu().numpy(), rtol=0, atol=0)
-        y = ql(X[0])
+        # stored codes + fp16 scales/zeros (the reference's buffer dtype) and
+        # the act-order g_idx reproduce the dequantized layer weight up to the
+        # fp16 rounding of the scales
+        np.testing.assert_array_equal(Wd.cpu().numpy(), O.dequant(
+            q.qcodes.cpu().numpy(), ql.scales.cpu().numpy(), ql.zeros.cpu().numpy(), q.g_idx.cpu().numpy()))
+        np.testing.assert_allclose(Wd.cpu().numpy(), lin.weight.data.float().cpu().numpy(), rtol=2e-3, atol=1e-4)
+        with torch.no_grad():
+            y = ql(X[0])
         ref = X[0].double().cpu().numpy() @ Wd.double().cpu().numpy().T + lin.bias.double().cpu().numpy()
         err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
         assert err < TOL[torch.float16]
