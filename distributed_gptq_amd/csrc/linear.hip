@@ -6,6 +6,10 @@
 // z * sum_k x_k) with exact small-integer codes in fp16/bf16 and fp32
 // accumulation, so a code costs one packed decode step and half a v_dot2.
 //
+//  * gemv_m1_k (M = 1): persistent workgroups; x staged once per workgroup in
+//    LDS in the order the packed words decode into fp16/bf16 pairs (one shift
+//    and one and-or per pair), each lane holding the x pairs of its 32-code
+//    chunks in registers across all rows it visits.
 //  * gemv_k (M <= 4): 4 waves per workgroup share x staged in LDS; a wave
 //    walks 4 weight rows at a time, lane l taking 128-bit chunks l, l+64, ...
 //    of each row (a wave load covers 1 KiB of contiguous codes).  Within a
@@ -228,6 +232,203 @@ __global__ __launch_bounds__(256) void gemv_k(LinArgs a) {
   }
 }
 
+// -------------------------------------------------------- M = 1 GEMV v2 --
+// 32-code chunks for every width (BITS dwords per chunk).  Pair p of a chunk
+// holds the codes (pair_a(p), pair_b(p)) -- the pairing one shift and one
+// and-or extract from the packed words -- and x is staged in the same order.
+template <int BITS>
+__host__ __device__ constexpr int pair_a(int p) {
+  return BITS == 4 ? 8 * (p / 4) + p % 4 : BITS == 2 ? 16 * (p / 8) + p % 8 : BITS == 8 ? 4 * (p / 2) + p % 2 : p;
+}
+template <int BITS>
+__host__ __device__ constexpr int pair_b(int p) {
+  return pair_a<BITS>(p) + (BITS == 4 ? 4 : BITS == 2 ? 8 : BITS == 8 ? 2 : 16);
+}
+
+template <int BITS, int P>
+__device__ __forceinline__ uint32_t pair32(const uint32_t* dw) {
+  if constexpr (BITS == 4) {
+    return (dw[P / 4] >> (4 * (P % 4))) & 0x000F000Fu;
+  } else if constexpr (BITS == 2) {
+    return (dw[P / 8] >> (2 * (P % 8))) & 0x00030003u;
+  } else if constexpr (BITS == 8) {
+    return (dw[P / 2] >> (8 * (P % 2))) & 0x00FF00FFu;
+  } else {
+    constexpr int b0 = 3 * P, b1 = 3 * P + 48;
+    constexpr int d0 = b0 / 32, o0 = b0 % 32, d1 = b1 / 32, o1 = b1 % 32;
+    uint32_t lo = dw[d0] >> o0;
+    if constexpr (o0 > 29 && d0 + 1 < 3) lo |= dw[d0 + 1] << (32 - o0);
+    uint32_t hi = dw[d1] >> o1;
+    if constexpr (o1 > 29 && d1 + 1 < 3) hi |= dw[d1 + 1] << (32 - o1);
+    return (lo & 7u) | ((hi & 7u) << 16);
+  }
+}
+
+// sum over the chunk of x * (code + offset): offset 1024 (fp16) or 128 (bf16,
+// widths < 8), 0 for 8-bit bf16 codes (converted exactly)
+template <int BITS, bool BF16, int P>
+__device__ __forceinline__ float dot_pair32(const uint32_t* dw, uint32_t xpair, float acc) {
+  const uint32_t c = pair32<BITS, P>(dw);
+  if constexpr (!BF16) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, c | 0x64006400u), __builtin_bit_cast(f16x2, xpair), acc,
+                                  false);
+  } else {
+    const uint32_t t = Magic<BITS, BF16>::kBF16Offset ? (c | 0x43004300u) : bf16_pair_exact(c);
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, t), __builtin_bit_cast(bf16x2, xpair), acc,
+                                           false);
+  }
+}
+
+template <int BITS, bool BF16, int... Ps>
+__device__ __forceinline__ float dot_chunk32(const uint32_t* dw, const uint32_t* xp, std::integer_sequence<int, Ps...>) {
+  float acc = 0.0f;
+  ((acc = dot_pair32<BITS, BF16, Ps>(dw, xp[Ps], acc)), ...);
+  return acc;
+}
+
+template <int BITS, bool BF16>
+struct Off32 {
+  static constexpr float v = BF16 ? Magic<BITS, BF16>::kOffset : 1024.0f;
+};
+
+// M = 1: persistent workgroups of 4 waves; x (pair order) and its 32-chunk
+// sums are staged in LDS once per workgroup, then each lane keeps the x pairs
+// of its chunks in registers for every row it visits.  WS = 1: every wave
+// walks its own rows, lane l taking chunks l, l + 64, ...; WS = 4 (long rows):
+// the four waves share each row, thread t taking chunks t, t + 256, ..., and
+// the partial sums meet in LDS.
+template <int BITS, bool BF16, int MAXC, int RB, int WS>
+__global__ __launch_bounds__(256) void gemv_m1_k(LinArgs a) {
+  extern __shared__ uint32_t lds[];
+  __shared__ float red[2][4][RB];
+  const int64_t K = a.K;
+  const int nch = static_cast<int>(K / 32);
+  uint32_t* xp_lds = lds;                                   // nch x 16 pair words
+  float* xs_lds = reinterpret_cast<float*>(lds + nch * 16);  // nch sums
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int me = WS == 4 ? tid : lane;
+  constexpr int kStride = 64 * WS;
+  const int64_t nbatches = cdiv(a.N, RB);
+  const int64_t step = WS == 4 ? gridDim.x : static_cast<int64_t>(gridDim.x) * 4;
+  int64_t rb = WS == 4 ? blockIdx.x : blockIdx.x * 4LL + wave;
+
+  for (int c = tid; c < nch; c += 256) {
+    uint16_t xv[32];
+    const u32x4* src = reinterpret_cast<const u32x4*>(a.x + static_cast<int64_t>(c) * 32);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const u32x4 t = src[v];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xv[8 * v + 2 * e] = static_cast<uint16_t>(t[e] & 0xffffu);
+        xv[8 * v + 2 * e + 1] = static_cast<uint16_t>(t[e] >> 16);
+      }
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) sum += BF16 ? bf16_bits_to_f32(xv[e]) : f16_bits_to_f32(xv[e]);
+    u32x4 o[4];
+#pragma unroll
+    for (int p = 0; p < 16; ++p)
+      o[p / 4][p % 4] = static_cast<uint32_t>(xv[pair_a<BITS>(p)]) | (static_cast<uint32_t>(xv[pair_b<BITS>(p)]) << 16);
+    u32x4* dst = reinterpret_cast<u32x4*>(xp_lds + c * 16);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) dst[v] = o[v];
+    xs_lds[c] = sum;
+  }
+  __syncthreads();
+
+  uint32_t xr[MAXC][16];
+  float xsr[MAXC];
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = me + kStride * i;
+    if (c < nch) {
+      const u32x4* srcv = reinterpret_cast<const u32x4*>(xp_lds + c * 16);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const u32x4 t = srcv[v];
+        xr[i][4 * v] = t[0]; xr[i][4 * v + 1] = t[1]; xr[i][4 * v + 2] = t[2]; xr[i][4 * v + 3] = t[3];
+      }
+      xsr[i] = xs_lds[c];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) xr[i][e] = 0u;
+      xsr[i] = 0.0f;
+    }
+  }
+
+  constexpr float off = Off32<BITS, BF16>::v;
+  int parity = 0;
+  for (; rb < nbatches; rb += step) {
+    const int64_t n0 = rb * RB;
+    uint32_t dw[RB][MAXC][BITS];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const int64_t n = std::min<int64_t>(n0 + r, a.N - 1);
+      const uint8_t* row = a.packed + n * a.pitch;
+#pragma unroll
+      for (int i = 0; i < MAXC; ++i) {
+        const int c = std::min(me + kStride * i, nch - 1);
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(row + static_cast<int64_t>(c) * (4 * BITS));
+        if constexpr (BITS % 4 == 0) {
+#pragma unroll
+          for (int v = 0; v < BITS / 4; ++v) {
+            const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + v);
+            dw[r][i][4 * v] = t[0]; dw[r][i][4 * v + 1] = t[1]; dw[r][i][4 * v + 2] = t[2]; dw[r][i][4 * v + 3] = t[3];
+          }
+        } else if constexpr (BITS == 2) {
+          const u32x2 t = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src));
+          dw[r][i][0] = t[0]; dw[r][i][1] = t[1];
+        } else {
+#pragma unroll
+          for (int v = 0; v < 3; ++v) dw[r][i][v] = __builtin_nontemporal_load(src + v);
+        }
+      }
+    }
+    float acc[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const int64_t n = std::min<int64_t>(n0 + r, a.N - 1);
+      float sacc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < MAXC; ++i) {
+        const int c = me + kStride * i;
+        if (c < nch) {
+          const int64_t g = (static_cast<int64_t>(c) * 32) / a.gs;
+          const float s = load_elem(a.scales, n * a.ngroups + g, a.sz_dtype);
+          const float z = load_elem(a.zeros, n * a.ngroups + g, a.sz_dtype);
+          const float d = dot_chunk32<BITS, BF16>(dw[r][i], xr[i], std::make_integer_sequence<int, 16>{});
+          sacc += s * (d - (z + off) * xsr[i]);
+        }
+      }
+      acc[r] = wave_sum(sacc);
+    }
+    if constexpr (WS == 4) {
+      if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < RB; ++r) red[parity][wave][r] = acc[r];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < RB; ++r)
+        acc[r] = red[parity][0][r] + red[parity][1][r] + red[parity][2][r] + red[parity][3][r];
+      parity ^= 1;
+    }
+    if (lane == 0 && (WS == 1 || wave == 0)) {
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const int64_t n = n0 + r;
+        if (n >= a.N) continue;
+        const float b = a.bias ? load_elem(a.bias, n, a.bias_dtype) : 0.0f;
+        store_elem(a.y, n, a.y_dtype, acc[r] + b);
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------ MFMA path ----
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
@@ -409,10 +610,28 @@ __global__ __launch_bounds__(256) void linear_generic(const void* __restrict__ x
   }
 }
 
+template <int BITS, bool BF16, int MAXC, int WS>
+int launch_m1(hipStream_t st, const LinArgs& a) {
+  constexpr int RB = BITS == 8 ? (MAXC >= 2 ? 2 : 4) : (MAXC >= 2 ? 4 : 8);
+  const int64_t nbatches = cdiv(a.N, RB);
+  const int64_t per_wg = WS == 4 ? 1 : 4;
+  const unsigned blocks = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(cdiv(nbatches, per_wg), 1024)));
+  const size_t lds = static_cast<size_t>(a.K / 32) * (16 * 4 + 4);
+  hipLaunchKernelGGL((gemv_m1_k<BITS, BF16, MAXC, RB, WS>), dim3(blocks), dim3(256), lds, st, a);
+  return check_launch("gemv_m1");
+}
+
 template <int BITS, bool BF16>
 int launch_fast(hipStream_t st, const LinArgs& a) {
   using F = Fmt<BITS>;
   const int64_t nch = a.K / F::CB;
+  if (a.M == 1 && a.K % 32 == 0 && a.gs % 32 == 0 && a.K <= 4 * 256 * 32) {
+    const int64_t nch32 = a.K / 32;
+    if (nch32 <= 64) return launch_m1<BITS, BF16, 1, 1>(st, a);
+    if (nch32 <= 128) return launch_m1<BITS, BF16, 2, 1>(st, a);
+    if (nch32 <= 512) return launch_m1<BITS, BF16, 2, 4>(st, a);
+    return launch_m1<BITS, BF16, 4, 4>(st, a);
+  }
   if (a.M <= 4) {
     const size_t lds = static_cast<size_t>(a.M) * a.K * 2 + static_cast<size_t>(a.M) * nch * 4;
     if (lds <= 64 * 1024) {

@@ -217,6 +217,110 @@ __global__ __launch_bounds__(256) void sweep_sub(SubArgs a) {
   }
 }
 
+// ------------------------------------------------ lanes-own-rows sweep --
+// Lane = row: every lane quantises its own row, so no work is discarded.  A
+// wave's 64 rows x n (<= 128) columns live column-major in LDS (ws[c][lane],
+// conflict-free); T^T of the sub-block is staged once per workgroup
+// (Tt[c][r] = T[r][c]).  Columns are processed in 32-wide panels: the panel
+// is held in registers and swept with a fully unrolled 32-step loop (T values
+// are LDS broadcast reads), then every later column of the sub-block takes
+// the panel's rank-32 update as a 32-term dot product.
+constexpr int kPW = 32;
+constexpr int kRowWaves = 2;  // waves (64 rows each) per workgroup
+constexpr int kTt = 132;      // row pitch of Tt in floats (16-byte aligned)
+constexpr int kMaxG = 6;      // groups a 128-column sub-block can touch for g >= 32
+
+__global__ __launch_bounds__(64 * kRowWaves) void sweep_rows(SubArgs a) {
+  extern __shared__ float smem[];
+  float* Tt = smem;                                   // 128 x kTt
+  float* ws_all = smem + 128 * kTt;                   // [wave][128][64]
+  float* prm_all = ws_all + kRowWaves * 128 * 64;     // [wave][kMaxG][2][64]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int n = a.n;
+  float* ws = ws_all + wave * 128 * 64;
+  float* prm = prm_all + wave * kMaxG * 2 * 64;
+
+  for (int e = tid; e < n * n; e += 64 * kRowWaves) {
+    const int r = e / n, c = e - (e / n) * n;
+    Tt[c * kTt + r] = a.T[(a.j1 + r) * a.ldt + a.j1 + c];
+  }
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (64 * kRowWaves) + wave * 64 + lane;
+  const bool valid = row < a.rows;
+  const int64_t rrow = valid ? row : a.rows - 1;
+  {
+    const float* src = a.W + rrow * a.cols + a.j1;
+    for (int c = 0; c < n; ++c) ws[c * 64 + lane] = src[c];
+  }
+  for (int g = 0; g < a.G; ++g) {
+    prm[(g * 2) * 64 + lane] = a.scale[rrow * a.ngroups + a.g_lo + g];
+    prm[(g * 2 + 1) * 64 + lane] = a.zero[rrow * a.ngroups + a.g_lo + g];
+  }
+  __syncthreads();
+
+  const float fmaxq = static_cast<float>(a.maxq);
+  float esq = 0.0f;
+  for (int p0 = 0; p0 < n; p0 += kPW) {
+    float wp[kPW], ep[kPW], qp[kPW], dp[kPW], lp[kPW];
+#pragma unroll
+    for (int i = 0; i < kPW; ++i) wp[i] = (p0 + i < n) ? ws[(p0 + i) * 64 + lane] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPW; ++i) {
+      const int j = p0 + i;
+      ep[i] = qp[i] = dp[i] = lp[i] = 0.0f;
+      if (j < n) {
+        const int g = a.gs > 0 ? static_cast<int>((a.j1 + j) / a.gs - a.g_lo) : 0;
+        const float s = prm[(g * 2) * 64 + lane];
+        const float z = prm[(g * 2 + 1) * 64 + lane];
+        const float w = wp[i];
+        float q;
+        if (a.ref)
+          q = fminf(fmaxf(rintf(w / s + z), 0.0f), fmaxq);
+        else
+          q = fminf(fmaxf(rintf(w / s) + z, 0.0f), fmaxq);
+        const float dq = s * (q - z);
+        const float d = Tt[j * kTt + j];
+        const float diff = w - dq;
+        const float e = diff / d;
+        ep[i] = e;
+        qp[i] = q;
+        dp[i] = dq;
+        lp[i] = diff * diff / (d * d) * 0.5f;
+        esq += e * e;
+#pragma unroll
+        for (int c = i + 1; c < kPW; ++c) wp[c] -= e * Tt[(p0 + c) * kTt + j];
+      }
+    }
+    // rank-32 update of the rest of the sub-block
+    for (int c = p0 + kPW; c < n; ++c) {
+      const f32x4* tv = reinterpret_cast<const f32x4*>(Tt + c * kTt + p0);
+      float acc = 0.0f;
+#pragma unroll
+      for (int v = 0; v < kPW / 4; ++v) {
+        const f32x4 t = tv[v];
+        acc += ep[4 * v] * t[0] + ep[4 * v + 1] * t[1] + ep[4 * v + 2] * t[2] + ep[4 * v + 3] * t[3];
+      }
+      ws[c * 64 + lane] -= acc;
+    }
+    if (valid) {
+#pragma unroll
+      for (int i = 0; i < kPW; ++i) {
+        const int j = p0 + i;
+        if (j < n) {
+          const int64_t gc = a.j1 + j;
+          const int64_t oc = a.out_cols ? a.out_cols[gc] : gc;
+          a.codes[row * a.cols + oc] = static_cast<uint8_t>(qp[i]);
+          if (a.dq) store_elem(a.dq, row * a.cols + oc, a.dq_dtype, dp[i]);
+          if (a.losses) a.losses[row * a.cols + oc] = lp[i];
+          if (a.Err) a.Err[row * a.lde + a.e_off + j] = ep[i];
+        }
+      }
+    }
+  }
+  if (valid && a.err_sq) a.err_sq[row] += esq;
+}
+
 __global__ void fill_zero_f(float* __restrict__ p, int64_t n) {
   for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x)
@@ -261,6 +365,13 @@ __global__ void prepare_weight_k(const void* __restrict__ w, int dtype, int64_t 
     if (dead && dead[pc]) v = 0.0f;
     out[idx] = v;
   }
+}
+
+int launch_rows(hipStream_t st, const SubArgs& a) {
+  const unsigned blocks = static_cast<unsigned>(cdiv(a.rows, 64LL * kRowWaves));
+  const size_t lds = sizeof(float) * (128 * kTt + kRowWaves * 128 * 64 + kRowWaves * kMaxG * 2 * 64);
+  hipLaunchKernelGGL(sweep_rows, dim3(blocks), dim3(64 * kRowWaves), lds, st, a);
+  return check_launch("sweep_rows");
 }
 
 template <int R, int NC>
@@ -383,9 +494,15 @@ extern "C" int gptq_quantize_sweep(float* W, const float* W0, const float* T, in
       a.out_cols = out_cols; a.codes = codes; a.dq = dequant; a.dq_dtype = dequant_dtype;
       a.err_sq = err_sq; a.losses = losses; a.Err = Err; a.lde = kSub; a.e_off = 0;
       const bool wide = n > 64;
-      if (R == 4) rc = wide ? launch_sub<4, 2>(st, a) : launch_sub<4, 1>(st, a);
-      else if (R == 2) rc = wide ? launch_sub<2, 2>(st, a) : launch_sub<2, 1>(st, a);
-      else rc = wide ? launch_sub<1, 2>(st, a) : launch_sub<1, 1>(st, a);
+      if (a.G <= kMaxG) {
+        rc = launch_rows(st, a);
+      } else if (R == 4) {
+        rc = wide ? launch_sub<4, 2>(st, a) : launch_sub<4, 1>(st, a);
+      } else if (R == 2) {
+        rc = wide ? launch_sub<2, 2>(st, a) : launch_sub<2, 1>(st, a);
+      } else {
+        rc = wide ? launch_sub<1, 2>(st, a) : launch_sub<1, 1>(st, a);
+      }
       if (rc) return rc;
       const int64_t end = trailing ? cols : i2;
       if (j2 < end) {

@@ -79,6 +79,22 @@ def test_linear_fast_paths(hip, xdt, bits, M):
     assert err < TOL[xdt], err
 
 
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+@pytest.mark.parametrize("K,gs", [(1024, 128), (4096, 128), (6144, 64), (14336, 128), (20480, 32)])
+def test_linear_m1_gemv(hip, xdt, bits, K, gs):
+    """M = 1 kernel in each regime: one or two chunks per lane, and the
+    four-wave split of long rows."""
+    from distributed_gptq_amd import _ops
+    N = 37
+    codes, scales, zeros, x = _case(1, N, K, bits, gs, K + bits, xdt)
+    packed = torch.from_numpy(O.pack_bitstream(codes, bits)).cuda()
+    y = _ops.linear(x.cuda(), packed, bits, scales.cuda(), zeros.cuda(), K, group_size=gs)
+    ref = O.linear(x.float().numpy(), codes, scales.numpy(), zeros.numpy(), np.arange(K) // gs)
+    err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err < TOL[xdt], err
+
+
 @pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
 def test_linear_generic_path_gidx_and_fp32(hip, xdt):
     """act-order g_idx gather and fp32 activations take the generic kernel."""
