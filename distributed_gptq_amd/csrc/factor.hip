@@ -13,13 +13,13 @@
 //                L22 = chol(S),  X22 = L22^-1            (recursion)
 //                X21 = -X22 (L21 X11)                    (2 GEMMs)
 // so that almost all of the 2K^3/3 flops run in large fp32-MFMA GEMMs; the
-// 64 x 64 leaves are factorised and inverted in LDS by one workgroup.
+// 128 x 128 leaves are factorised and inverted in LDS by one workgroup.
 #include "gemm.hpp"
 
 namespace gptq {
 namespace {
 
-constexpr int kNB = 64;  // leaf size
+constexpr int kNB = 128;  // leaf size (one workgroup, in LDS)
 
 // mean of the (possibly dead-fixed) scaled diagonal -> lambda; dead flags
 __global__ __launch_bounds__(1024) void diag_stats(const float* __restrict__ H, int64_t K, float scale,
@@ -82,54 +82,81 @@ __global__ void fill_zero(float* __restrict__ p, int64_t n) {
     p[i] = 0.0f;
 }
 
-// One workgroup: Cholesky of the m x m (m <= 64) diagonal block of A at
-// (n0, n0) and the inverse of its factor.  Writes L (zeros above) into A and
-// X = L^-1 (zeros above) into X.  A non-positive pivot records
-// info = 1 + (index of the column in A order) once.
-__global__ __launch_bounds__(256) void chol_inv_leaf(float* __restrict__ A, float* __restrict__ X, int64_t ld,
-                                                     int64_t n0, int m, int32_t* __restrict__ info) {
-  __shared__ float a[kNB][kNB + 1];
-  __shared__ float x[kNB][kNB + 1];
+// One workgroup of 1024 threads: Cholesky of the m x m (m <= 128) diagonal
+// block of A at (n0, n0) and the inverse of its factor, both right-looking in
+// LDS.  Thread (ti, tk) of a 32 x 32 grid owns rows 4*ti..4*ti+3 and columns
+// 4*tk..4*tk+3, so every rank-1 update is 16 FMAs per thread with no index
+// arithmetic beyond shifts.  Writes L (zeros above) into A and X = L^-1
+// (zeros above) into X.  A non-positive pivot records info = 1 + (column in A
+// order) once.
+constexpr int kLP = kNB + 1;  // LDS pitch
+
+__global__ __launch_bounds__(1024) void chol_inv_leaf(float* __restrict__ A, float* __restrict__ X, int64_t ld,
+                                                      int64_t n0, int m, int32_t* __restrict__ info) {
+  extern __shared__ float lds[];
+  float* a = lds;             // kNB x kLP
+  float* x = lds + kNB * kLP;  // kNB x kLP
   const int tid = threadIdx.x;
-  for (int e = tid; e < kNB * kNB; e += 256) {
-    const int i = e / kNB, j = e % kNB;
-    a[i][j] = (i < m && j <= i) ? A[(n0 + i) * ld + n0 + j] : 0.0f;
-    x[i][j] = 0.0f;
+  const int ti = tid >> 5, tk = tid & 31;
+  for (int e = tid; e < kNB * kNB; e += 1024) {
+    const int i = e >> 7, j = e & (kNB - 1);
+    a[i * kLP + j] = (i < m && j <= i) ? A[(n0 + i) * ld + n0 + j] : 0.0f;
+    x[i * kLP + j] = (i == j && i < m) ? 1.0f : 0.0f;
   }
   __syncthreads();
-  bool failed = false;
+  int first_bad = -1;
   for (int j = 0; j < m; ++j) {
-    const float p = a[j][j];
+    const float p = a[j * kLP + j];
     const float d = sqrtf(p);
-    if (!(p > 0.0f)) failed = true;
+    if (!(p > 0.0f) && first_bad < 0) first_bad = j;
+    if (tid > j && tid < m) a[tid * kLP + j] /= d;
     __syncthreads();
-    for (int i = j + 1 + tid; i < m; i += 256) a[i][j] /= d;
-    if (tid == 0) a[j][j] = d;
-    __syncthreads();
-    // trailing update of the lower triangle: a[i][k] -= a[i][j] a[k][j], j < k <= i
-    const int t = m - j - 1;
-    for (int e = tid; e < t * t; e += 256) {
-      const int i = j + 1 + e / t, k = j + 1 + e % t;
-      if (k <= i) a[i][k] -= a[i][j] * a[k][j];
+    if (tid == 0) a[j * kLP + j] = d;
+    float ar[4], ac[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      ar[u] = a[(4 * ti + u) * kLP + j];
+      ac[u] = a[(4 * tk + u) * kLP + j];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int r = 4 * ti + u;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int c = 4 * tk + v;
+        if (r > j && c > j && c <= r) a[r * kLP + c] -= ar[u] * ac[v];
+      }
     }
     __syncthreads();
   }
-  if (failed && tid == 0) atomicCAS(info, 0, static_cast<int32_t>(n0 + 1));
-  // inverse: column c, forward substitution x[i][c] = -(sum_{k=c}^{i-1} a[i][k] x[k][c]) / a[i][i]
-  if (tid < m) {
-    const int c = tid;
-    x[c][c] = 1.0f / a[c][c];
-    for (int i = c + 1; i < m; ++i) {
-      float s = 0.0f;
-      for (int k = c; k < i; ++k) s += a[i][k] * x[k][c];
-      x[i][c] = -s / a[i][i];
+  if (first_bad >= 0 && tid == 0) atomicCAS(info, 0, static_cast<int32_t>(n0 + first_bad + 1));
+  // X = L^-1, right-looking: row j of X scaled by 1/L[j][j], then subtracted
+  // from the rows below with weights L[r][j]
+  for (int j = 0; j < m; ++j) {
+    const float dj = a[j * kLP + j];
+    if (tid <= j) x[j * kLP + tid] /= dj;
+    __syncthreads();
+    float lr[4], xc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      lr[u] = a[(4 * ti + u) * kLP + j];
+      xc[u] = x[j * kLP + 4 * tk + u];
     }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int r = 4 * ti + u;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int c = 4 * tk + v;
+        if (r > j && r < m && c <= j) x[r * kLP + c] -= lr[u] * xc[v];
+      }
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  for (int e = tid; e < m * m; e += 256) {
-    const int i = e / m, j = e % m;
-    A[(n0 + i) * ld + n0 + j] = (j <= i) ? a[i][j] : 0.0f;
-    X[(n0 + i) * ld + n0 + j] = (j <= i) ? x[i][j] : 0.0f;
+  for (int e = tid; e < m * m; e += 1024) {
+    const int i = e / m, j = e - (e / m) * m;
+    A[(n0 + i) * ld + n0 + j] = (j <= i) ? a[i * kLP + j] : 0.0f;
+    X[(n0 + i) * ld + n0 + j] = (j <= i) ? x[i * kLP + j] : 0.0f;
   }
 }
 
@@ -183,7 +210,8 @@ int64_t scratch_floats(int64_t m) {
 int chol_inv(Ctx& c, int64_t n0, int64_t m, float* tmp) {
   const int64_t ld = c.K;
   if (m <= kNB) {
-    hipLaunchKernelGGL(chol_inv_leaf, dim3(1), dim3(256), 0, c.st, c.A, c.X, ld, n0, static_cast<int>(m), c.info);
+    hipLaunchKernelGGL(chol_inv_leaf, dim3(1), dim3(1024), 2 * kNB * kLP * sizeof(float), c.st, c.A, c.X, ld, n0,
+                       static_cast<int>(m), c.info);
     return check_launch("chol_inv_leaf");
   }
   const int64_t m1 = split_of(m), m2 = m - m1;

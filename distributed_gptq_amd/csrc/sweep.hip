@@ -228,7 +228,7 @@ __global__ __launch_bounds__(256) void sweep_sub(SubArgs a) {
 constexpr int kPW = 32;
 constexpr int kRowWaves = 2;  // waves (64 rows each) per workgroup
 constexpr int kTt = 132;      // row pitch of Tt in floats (16-byte aligned)
-constexpr int kMaxG = 6;      // groups a 128-column sub-block can touch for g >= 32
+constexpr int kMaxG = 6;      // groups a 128-column sub-block can touch when g >= 32
 
 __global__ __launch_bounds__(64 * kRowWaves) void sweep_rows(SubArgs a) {
   extern __shared__ float smem[];
@@ -251,7 +251,17 @@ __global__ __launch_bounds__(64 * kRowWaves) void sweep_rows(SubArgs a) {
   const int64_t rrow = valid ? row : a.rows - 1;
   {
     const float* src = a.W + rrow * a.cols + a.j1;
-    for (int c = 0; c < n; ++c) ws[c * 64 + lane] = src[c];
+    int c = 0;
+    if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+      for (; c + 4 <= n; c += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(src + c);
+        ws[c * 64 + lane] = v[0];
+        ws[(c + 1) * 64 + lane] = v[1];
+        ws[(c + 2) * 64 + lane] = v[2];
+        ws[(c + 3) * 64 + lane] = v[3];
+      }
+    }
+    for (; c < n; ++c) ws[c * 64 + lane] = src[c];
   }
   for (int g = 0; g < a.G; ++g) {
     prm[(g * 2) * 64 + lane] = a.scale[rrow * a.ngroups + a.g_lo + g];
@@ -260,20 +270,40 @@ __global__ __launch_bounds__(64 * kRowWaves) void sweep_rows(SubArgs a) {
   __syncthreads();
 
   const float fmaxq = static_cast<float>(a.maxq);
+  const int gs = a.gs;
+  const int j1 = static_cast<int>(a.j1 - a.g_lo * static_cast<int64_t>(gs > 0 ? gs : 0));  // offset in group 0
   float esq = 0.0f;
   for (int p0 = 0; p0 < n; p0 += kPW) {
-    float wp[kPW], ep[kPW], qp[kPW], dp[kPW], lp[kPW];
-#pragma unroll
-    for (int i = 0; i < kPW; ++i) wp[i] = (p0 + i < n) ? ws[(p0 + i) * 64 + lane] : 0.0f;
+    // groups of this panel: g0 for columns before `brk`, g0 + 1 after (g >= 32)
+    int g0 = 0, brk = kPW;
+    if (gs > 0) {
+      g0 = (j1 + p0) / gs;
+      brk = (g0 + 1) * gs - (j1 + p0);
+    }
+    const float s0 = prm[(g0 * 2) * 64 + lane], z0 = prm[(g0 * 2 + 1) * 64 + lane];
+    const int g1 = (g0 + 1 < a.G) ? g0 + 1 : g0;
+    const float s1 = prm[(g1 * 2) * 64 + lane], z1 = prm[(g1 * 2 + 1) * 64 + lane];
+    float ep[kPW], qp[kPW], dp[kPW], lp[kPW];
 #pragma unroll
     for (int i = 0; i < kPW; ++i) {
       const int j = p0 + i;
       ep[i] = qp[i] = dp[i] = lp[i] = 0.0f;
       if (j < n) {
-        const int g = a.gs > 0 ? static_cast<int>((a.j1 + j) / a.gs - a.g_lo) : 0;
-        const float s = prm[(g * 2) * 64 + lane];
-        const float z = prm[(g * 2 + 1) * 64 + lane];
-        const float w = wp[i];
+        // left-looking: apply the panel's earlier errors to column j
+        float w = ws[j * 64 + lane];
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const f32x4* trow = reinterpret_cast<const f32x4*>(Tt + j * kTt + p0);
+#pragma unroll
+        for (int k4 = 0; k4 < (i + 3) / 4; ++k4) {
+          const f32x4 t = trow[k4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            if (4 * k4 + u < i) acc[u] += ep[4 * k4 + u] * t[u];
+        }
+        w -= (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        const bool second = i >= brk;
+        const float s = second ? s1 : s0;
+        const float z = second ? z1 : z0;
         float q;
         if (a.ref)
           q = fminf(fmaxf(rintf(w / s + z), 0.0f), fmaxq);
@@ -288,32 +318,68 @@ __global__ __launch_bounds__(64 * kRowWaves) void sweep_rows(SubArgs a) {
         dp[i] = dq;
         lp[i] = diff * diff / (d * d) * 0.5f;
         esq += e * e;
-#pragma unroll
-        for (int c = i + 1; c < kPW; ++c) wp[c] -= e * Tt[(p0 + c) * kTt + j];
       }
     }
     // rank-32 update of the rest of the sub-block
     for (int c = p0 + kPW; c < n; ++c) {
       const f32x4* tv = reinterpret_cast<const f32x4*>(Tt + c * kTt + p0);
-      float acc = 0.0f;
+      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int v = 0; v < kPW / 4; ++v) {
         const f32x4 t = tv[v];
-        acc += ep[4 * v] * t[0] + ep[4 * v + 1] * t[1] + ep[4 * v + 2] * t[2] + ep[4 * v + 3] * t[3];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[u] += ep[4 * v + u] * t[u];
       }
-      ws[c * 64 + lane] -= acc;
+      ws[c * 64 + lane] -= (acc[0] + acc[1]) + (acc[2] + acc[3]);
     }
     if (valid) {
+      const int64_t gc0 = a.j1 + p0;
+      const bool full = p0 + kPW <= n;
+      const bool vec = full && !a.out_cols && ((row * a.cols + gc0) & 15) == 0;
+      if (vec) {
+        u32x4 cw[2];
 #pragma unroll
-      for (int i = 0; i < kPW; ++i) {
-        const int j = p0 + i;
-        if (j < n) {
-          const int64_t gc = a.j1 + j;
-          const int64_t oc = a.out_cols ? a.out_cols[gc] : gc;
-          a.codes[row * a.cols + oc] = static_cast<uint8_t>(qp[i]);
-          if (a.dq) store_elem(a.dq, row * a.cols + oc, a.dq_dtype, dp[i]);
-          if (a.losses) a.losses[row * a.cols + oc] = lp[i];
-          if (a.Err) a.Err[row * a.lde + a.e_off + j] = ep[i];
+        for (int v = 0; v < 8; ++v) {
+          const uint32_t w4 = static_cast<uint32_t>(qp[4 * v]) | (static_cast<uint32_t>(qp[4 * v + 1]) << 8) |
+                              (static_cast<uint32_t>(qp[4 * v + 2]) << 16) |
+                              (static_cast<uint32_t>(qp[4 * v + 3]) << 24);
+          cw[v / 4][v % 4] = w4;
+        }
+        u32x4* cdst = reinterpret_cast<u32x4*>(a.codes + row * a.cols + gc0);
+        cdst[0] = cw[0];
+        cdst[1] = cw[1];
+        if (a.losses) {
+          f32x4* ldst = reinterpret_cast<f32x4*>(a.losses + row * a.cols + gc0);
+#pragma unroll
+          for (int v = 0; v < 8; ++v) ldst[v] = f32x4{lp[4 * v], lp[4 * v + 1], lp[4 * v + 2], lp[4 * v + 3]};
+        }
+        if (a.dq) {
+#pragma unroll
+          for (int i = 0; i < kPW; ++i) store_elem(a.dq, row * a.cols + gc0 + i, a.dq_dtype, dp[i]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < kPW; ++i) {
+          const int j = p0 + i;
+          if (j < n) {
+            const int64_t gc = a.j1 + j;
+            const int64_t oc = a.out_cols ? a.out_cols[gc] : gc;
+            a.codes[row * a.cols + oc] = static_cast<uint8_t>(qp[i]);
+            if (a.dq) store_elem(a.dq, row * a.cols + oc, a.dq_dtype, dp[i]);
+            if (a.losses) a.losses[row * a.cols + oc] = lp[i];
+          }
+        }
+      }
+      if (a.Err) {
+        float* edst = a.Err + row * a.lde + a.e_off + p0;
+        if (full && ((reinterpret_cast<uintptr_t>(edst) & 15) == 0)) {
+#pragma unroll
+          for (int v = 0; v < 8; ++v)
+            reinterpret_cast<f32x4*>(edst)[v] = f32x4{ep[4 * v], ep[4 * v + 1], ep[4 * v + 2], ep[4 * v + 3]};
+        } else {
+#pragma unroll
+          for (int i = 0; i < kPW; ++i)
+            if (p0 + i < n) edst[i] = ep[i];
         }
       }
     }
@@ -494,7 +560,8 @@ extern "C" int gptq_quantize_sweep(float* W, const float* W0, const float* T, in
       a.out_cols = out_cols; a.codes = codes; a.dq = dequant; a.dq_dtype = dequant_dtype;
       a.err_sq = err_sq; a.losses = losses; a.Err = Err; a.lde = kSub; a.e_off = 0;
       const bool wide = n > 64;
-      if (a.G <= kMaxG) {
+      if ((gs <= 0 || gs >= kPW) && a.G <= kMaxG) {
+        // one group boundary at most per 32-column panel
         rc = launch_rows(st, a);
       } else if (R == 4) {
         rc = wide ? launch_sub<4, 2>(st, a) : launch_sub<4, 1>(st, a);
