@@ -13,13 +13,13 @@
 //                L22 = chol(S),  X22 = L22^-1            (recursion)
 //                X21 = -X22 (L21 X11)                    (2 GEMMs)
 // so that almost all of the 2K^3/3 flops run in large fp32-MFMA GEMMs; the
-// 128 x 128 leaves are factorised and inverted in LDS by one workgroup.
+// 64 x 64 leaves are factorised and inverted in LDS by one workgroup.
 #include "gemm.hpp"
 
 namespace gptq {
 namespace {
 
-constexpr int kNB = 128;  // leaf size (one workgroup, in LDS)
+constexpr int kNB = 64;  // leaf size (one workgroup, in LDS)
 
 // mean of the (possibly dead-fixed) scaled diagonal -> lambda; dead flags
 __global__ __launch_bounds__(1024) void diag_stats(const float* __restrict__ H, int64_t K, float scale,
@@ -82,24 +82,24 @@ __global__ void fill_zero(float* __restrict__ p, int64_t n) {
     p[i] = 0.0f;
 }
 
-// One workgroup of 1024 threads: Cholesky of the m x m (m <= 128) diagonal
+// One workgroup of 256 threads: Cholesky of the m x m (m <= 64) diagonal
 // block of A at (n0, n0) and the inverse of its factor, both right-looking in
-// LDS.  Thread (ti, tk) of a 32 x 32 grid owns rows 4*ti..4*ti+3 and columns
+// LDS.  Thread (ti, tk) of a 16 x 16 grid owns rows 4*ti..4*ti+3 and columns
 // 4*tk..4*tk+3, so every rank-1 update is 16 FMAs per thread with no index
 // arithmetic beyond shifts.  Writes L (zeros above) into A and X = L^-1
 // (zeros above) into X.  A non-positive pivot records info = 1 + (column in A
 // order) once.
 constexpr int kLP = kNB + 1;  // LDS pitch
 
-__global__ __launch_bounds__(1024) void chol_inv_leaf(float* __restrict__ A, float* __restrict__ X, int64_t ld,
+__global__ __launch_bounds__(256) void chol_inv_leaf(float* __restrict__ A, float* __restrict__ X, int64_t ld,
                                                       int64_t n0, int m, int32_t* __restrict__ info) {
   extern __shared__ float lds[];
   float* a = lds;             // kNB x kLP
   float* x = lds + kNB * kLP;  // kNB x kLP
   const int tid = threadIdx.x;
-  const int ti = tid >> 5, tk = tid & 31;
-  for (int e = tid; e < kNB * kNB; e += 1024) {
-    const int i = e >> 7, j = e & (kNB - 1);
+  const int ti = tid >> 4, tk = tid & 15;
+  for (int e = tid; e < kNB * kNB; e += 256) {
+    const int i = e >> 6, j = e & (kNB - 1);
     a[i * kLP + j] = (i < m && j <= i) ? A[(n0 + i) * ld + n0 + j] : 0.0f;
     x[i * kLP + j] = (i == j && i < m) ? 1.0f : 0.0f;
   }
@@ -153,8 +153,9 @@ __global__ __launch_bounds__(1024) void chol_inv_leaf(float* __restrict__ A, flo
     }
     __syncthreads();
   }
-  for (int e = tid; e < m * m; e += 1024) {
-    const int i = e / m, j = e - (e / m) * m;
+  for (int e = tid; e < kNB * kNB; e += 256) {
+    const int i = e >> 6, j = e & (kNB - 1);
+    if (i >= m || j >= m) continue;
     A[(n0 + i) * ld + n0 + j] = (j <= i) ? a[i * kLP + j] : 0.0f;
     X[(n0 + i) * ld + n0 + j] = (j <= i) ? x[i * kLP + j] : 0.0f;
   }
@@ -210,7 +211,7 @@ int64_t scratch_floats(int64_t m) {
 int chol_inv(Ctx& c, int64_t n0, int64_t m, float* tmp) {
   const int64_t ld = c.K;
   if (m <= kNB) {
-    hipLaunchKernelGGL(chol_inv_leaf, dim3(1), dim3(1024), 2 * kNB * kLP * sizeof(float), c.st, c.A, c.X, ld, n0,
+    hipLaunchKernelGGL(chol_inv_leaf, dim3(1), dim3(256), 2 * kNB * kLP * sizeof(float), c.st, c.A, c.X, ld, n0,
                        static_cast<int>(m), c.info);
     return check_launch("chol_inv_leaf");
   }

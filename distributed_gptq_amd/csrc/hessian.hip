@@ -42,7 +42,7 @@ __device__ __forceinline__ void tile_coords(int t, int& I, int& J) {
 __device__ __forceinline__ int swz(int f) { return f ^ ((f >> 4) & 15); }
 
 // ------------------------------------------------------- 16-bit inputs ----
-// LDS: [operand][token-octet (8)][slot (256)] x 16 B  (8 tokens of a feature)
+// LDS: [buffer][operand][token-octet (8)][slot (256)] x 16 B  (8 tokens of a feature)
 // 64 tokens per stage; 512 loader threads = 2 operands x 8 token-octets x 32
 // feature-octets, one 8x8 block each.
 template <bool kBF16, bool kVec>
@@ -50,7 +50,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 void hessian_tile16(const uint16_t* __restrict__ X, int64_t n, int K, int64_t ldx,
                     int S, int64_t tok_per_split, int ntiles, float* __restrict__ partial) {
   constexpr int kBK = 64;
-  __shared__ u32x4 lds[2][kBK / 8][kTile];
+  __shared__ u32x4 lds[2][2][kBK / 8][kTile];  // [buffer][operand][token-octet][slot]
 
   const int s = blockIdx.x % S;
   const int tile = blockIdx.x / S;
@@ -103,7 +103,7 @@ void hessian_tile16(const uint16_t* __restrict__ X, int64_t n, int K, int64_t ld
       pre[r] = v;
     }
   };
-  auto store_stage = [&]() {
+  auto store_stage = [&](int bsel) {
     if (!loader) return;
 #pragma unroll
     for (int f = 0; f < 8; ++f) {
@@ -114,26 +114,31 @@ void hessian_tile16(const uint16_t* __restrict__ X, int64_t n, int K, int64_t ld
         const uint32_t b = pre[2 * d + 1][f >> 1];
         o[d] = (f & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
       }
-      lds[op][to][swz(fo * 8 + f)] = o;
+      lds[bsel][op][to][swz(fo * 8 + f)] = o;
     }
   };
 
+  // LDS ping-pong: stage s is multiplied out of buffer s & 1 while stage s + 1
+  // is written to the other buffer and stage s + 2 is being fetched; one
+  // barrier per stage.
   const int bop = diag ? 0 : 1;
-  if (t_begin < t_end) load_stage(t_begin);
+  int buf = 0;
+  if (t_begin < t_end) {
+    load_stage(t_begin);
+    store_stage(0);
+    if (t_begin + kBK < t_end) load_stage(t_begin + kBK);
+  }
+  __syncthreads();
   for (int64_t t0 = t_begin; t0 < t_end; t0 += kBK) {
-    __syncthreads();
-    store_stage();
-    __syncthreads();
-    if (t0 + kBK < t_end) load_stage(t0 + kBK);
     if (!wave_idle) {
 #pragma unroll
       for (int ks = 0; ks < kBK / 16; ++ks) {
         const int tko = ks * 2 + (lane >> 5);
         u32x4 a[4], b[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) a[i] = lds[0][tko][swz(wm + i * 32 + (lane & 31))];
+        for (int i = 0; i < 4; ++i) a[i] = lds[buf][0][tko][swz(wm + i * 32 + (lane & 31))];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) b[j] = lds[bop][tko][swz(wn + j * 32 + (lane & 31))];
+        for (int j = 0; j < 2; ++j) b[j] = lds[buf][bop][tko][swz(wn + j * 32 + (lane & 31))];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -148,6 +153,12 @@ void hessian_tile16(const uint16_t* __restrict__ X, int64_t n, int K, int64_t ld
           }
       }
     }
+    if (t0 + kBK < t_end) {
+      store_stage(buf ^ 1);
+      if (t0 + 2 * kBK < t_end) load_stage(t0 + 2 * kBK);
+    }
+    __syncthreads();
+    buf ^= 1;
   }
 
   // 32x32 accumulator layout: lane l, register v -> row 8*(v/4) + 4*(l/32) + v%4, col l%32

@@ -314,6 +314,41 @@ __global__ __launch_bounds__(256) void gemv_m1_k(LinArgs a) {
   const int64_t step = WS == 4 ? gridDim.x : static_cast<int64_t>(gridDim.x) * 4;
   int64_t rb = WS == 4 ? blockIdx.x : blockIdx.x * 4LL + wave;
 
+  // the weight stream does not depend on x: start the first batch's loads
+  // before x is staged
+  uint32_t dwA[RB][MAXC][BITS], dwB[RB][MAXC][BITS];
+  float sA[RB][MAXC], zA[RB][MAXC], sB[RB][MAXC], zB[RB][MAXC];
+  auto load_batch = [&](int64_t b, uint32_t (&dw)[RB][MAXC][BITS], float (&sc)[RB][MAXC], float (&zc)[RB][MAXC]) {
+    const int64_t n0 = b * RB;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const int64_t n = std::min<int64_t>(n0 + r, a.N - 1);
+      const uint8_t* row = a.packed + n * a.pitch;
+#pragma unroll
+      for (int i = 0; i < MAXC; ++i) {
+        const int c = std::min(me + kStride * i, nch - 1);
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(row + static_cast<int64_t>(c) * (4 * BITS));
+        if constexpr (BITS % 4 == 0) {
+#pragma unroll
+          for (int v = 0; v < BITS / 4; ++v) {
+            const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + v);
+            dw[r][i][4 * v] = t[0]; dw[r][i][4 * v + 1] = t[1]; dw[r][i][4 * v + 2] = t[2]; dw[r][i][4 * v + 3] = t[3];
+          }
+        } else if constexpr (BITS == 2) {
+          const u32x2 t = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src));
+          dw[r][i][0] = t[0]; dw[r][i][1] = t[1];
+        } else {
+#pragma unroll
+          for (int v = 0; v < 3; ++v) dw[r][i][v] = __builtin_nontemporal_load(src + v);
+        }
+        const int64_t g = (static_cast<int64_t>(c) * 32) / a.gs;
+        sc[r][i] = load_elem(a.scales, n * a.ngroups + g, a.sz_dtype);
+        zc[r][i] = load_elem(a.zeros, n * a.ngroups + g, a.sz_dtype);
+      }
+    }
+  };
+  if (rb < nbatches) load_batch(rb, dwA, sA, zA);
+
   for (int c = tid; c < nch; c += 256) {
     uint16_t xv[32];
     const u32x4* src = reinterpret_cast<const u32x4*>(a.x + static_cast<int64_t>(c) * 32);
@@ -362,46 +397,19 @@ __global__ __launch_bounds__(256) void gemv_m1_k(LinArgs a) {
 
   constexpr float off = Off32<BITS, BF16>::v;
   int parity = 0;
-  for (; rb < nbatches; rb += step) {
-    const int64_t n0 = rb * RB;
-    uint32_t dw[RB][MAXC][BITS];
-#pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      const int64_t n = std::min<int64_t>(n0 + r, a.N - 1);
-      const uint8_t* row = a.packed + n * a.pitch;
-#pragma unroll
-      for (int i = 0; i < MAXC; ++i) {
-        const int c = std::min(me + kStride * i, nch - 1);
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(row + static_cast<int64_t>(c) * (4 * BITS));
-        if constexpr (BITS % 4 == 0) {
-#pragma unroll
-          for (int v = 0; v < BITS / 4; ++v) {
-            const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + v);
-            dw[r][i][4 * v] = t[0]; dw[r][i][4 * v + 1] = t[1]; dw[r][i][4 * v + 2] = t[2]; dw[r][i][4 * v + 3] = t[3];
-          }
-        } else if constexpr (BITS == 2) {
-          const u32x2 t = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src));
-          dw[r][i][0] = t[0]; dw[r][i][1] = t[1];
-        } else {
-#pragma unroll
-          for (int v = 0; v < 3; ++v) dw[r][i][v] = __builtin_nontemporal_load(src + v);
-        }
-      }
-    }
+  auto compute = [&](int64_t b, const uint32_t (&dw)[RB][MAXC][BITS], const float (&sc)[RB][MAXC],
+                     const float (&zc)[RB][MAXC]) {
+    const int64_t n0 = b * RB;
     float acc[RB];
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-      const int64_t n = std::min<int64_t>(n0 + r, a.N - 1);
       float sacc = 0.0f;
 #pragma unroll
       for (int i = 0; i < MAXC; ++i) {
         const int c = me + kStride * i;
         if (c < nch) {
-          const int64_t g = (static_cast<int64_t>(c) * 32) / a.gs;
-          const float s = load_elem(a.scales, n * a.ngroups + g, a.sz_dtype);
-          const float z = load_elem(a.zeros, n * a.ngroups + g, a.sz_dtype);
           const float d = dot_chunk32<BITS, BF16>(dw[r][i], xr[i], std::make_integer_sequence<int, 16>{});
-          sacc += s * (d - (z + off) * xsr[i]);
+          sacc += sc[r][i] * (d - (zc[r][i] + off) * xsr[i]);
         }
       }
       acc[r] = wave_sum(sacc);
@@ -422,10 +430,22 @@ __global__ __launch_bounds__(256) void gemv_m1_k(LinArgs a) {
       for (int r = 0; r < RB; ++r) {
         const int64_t n = n0 + r;
         if (n >= a.N) continue;
-        const float b = a.bias ? load_elem(a.bias, n, a.bias_dtype) : 0.0f;
-        store_elem(a.y, n, a.y_dtype, acc[r] + b);
+        const float bias = a.bias ? load_elem(a.bias, n, a.bias_dtype) : 0.0f;
+        store_elem(a.y, n, a.y_dtype, acc[r] + bias);
       }
     }
+  };
+
+  // double-buffered walk over this wave's (or workgroup's) row batches
+  while (rb < nbatches) {
+    const int64_t nb1 = rb + step;
+    if (nb1 < nbatches) load_batch(nb1, dwB, sB, zB);
+    compute(rb, dwA, sA, zA);
+    if (nb1 >= nbatches) break;
+    const int64_t nb2 = nb1 + step;
+    if (nb2 < nbatches) load_batch(nb2, dwA, sA, zA);
+    compute(nb1, dwB, sB, zB);
+    rb = nb2;
   }
 }
 
