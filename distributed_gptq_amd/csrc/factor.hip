@@ -13,13 +13,13 @@
 //                L22 = chol(S),  X22 = L22^-1            (recursion)
 //                X21 = -X22 (L21 X11)                    (2 GEMMs)
 // so that almost all of the 2K^3/3 flops run in large fp32-MFMA GEMMs; the
-// 64 x 64 leaves are factorised and inverted in LDS by one workgroup.
+// 128 x 128 leaves are factorised and inverted by one workgroup.
 #include "gemm.hpp"
 
 namespace gptq {
 namespace {
 
-constexpr int kNB = 64;  // leaf size (one workgroup, in LDS)
+constexpr int kNB = 128;  // leaf size (one workgroup, registers + LDS)
 
 // mean of the (possibly dead-fixed) scaled diagonal -> lambda; dead flags
 __global__ __launch_bounds__(1024) void diag_stats(const float* __restrict__ H, int64_t K, float scale,
@@ -82,83 +82,145 @@ __global__ void fill_zero(float* __restrict__ p, int64_t n) {
     p[i] = 0.0f;
 }
 
-// One workgroup of 256 threads: Cholesky of the m x m (m <= 64) diagonal
-// block of A at (n0, n0) and the inverse of its factor, both right-looking in
-// LDS.  Thread (ti, tk) of a 16 x 16 grid owns rows 4*ti..4*ti+3 and columns
-// 4*tk..4*tk+3, so every rank-1 update is 16 FMAs per thread with no index
-// arithmetic beyond shifts.  Writes L (zeros above) into A and X = L^-1
-// (zeros above) into X.  A non-positive pivot records info = 1 + (column in A
-// order) once.
-constexpr int kLP = kNB + 1;  // LDS pitch
+// One workgroup of 256 threads: Cholesky of the m x m (m <= 128) diagonal
+// block of A at (n0, n0) and the inverse of its factor.  Thread (ti, tk) of a
+// 16 x 16 grid keeps rows 8*ti..8*ti+7, columns 8*tk..8*tk+7 of the block in
+// registers; each right-looking step publishes only the next pivot column
+// (Cholesky) or the next scaled row (inverse) through a double-buffered LDS
+// vector, so a step costs one barrier, 16 LDS reads and 64 FMAs per thread.
+// Writes L (zeros above) into A and X = L^-1 (zeros above) into X.  A
+// non-positive pivot records info = 1 + (column in A order) once.
+constexpr int kLP = kNB + 1;  // LDS pitch of L
+constexpr size_t kLeafLds = sizeof(float) * (2 * kNB + kNB * kLP + 2 * kNB);
 
 __global__ __launch_bounds__(256) void chol_inv_leaf(float* __restrict__ A, float* __restrict__ X, int64_t ld,
-                                                      int64_t n0, int m, int32_t* __restrict__ info) {
+                                                     int64_t n0, int m, int32_t* __restrict__ info) {
   extern __shared__ float lds[];
-  float* a = lds;             // kNB x kLP
-  float* x = lds + kNB * kLP;  // kNB x kLP
+  float* col = lds;                  // [2][kNB]
+  float* Ls = lds + 2 * kNB;         // [kNB][kLP]
+  float* xrow = Ls + kNB * kLP;      // [2][kNB]
   const int tid = threadIdx.x;
   const int ti = tid >> 4, tk = tid & 15;
-  for (int e = tid; e < kNB * kNB; e += 256) {
-    const int i = e >> 6, j = e & (kNB - 1);
-    a[i * kLP + j] = (i < m && j <= i) ? A[(n0 + i) * ld + n0 + j] : 0.0f;
-    x[i * kLP + j] = (i == j && i < m) ? 1.0f : 0.0f;
+  const int R0 = 8 * ti, C0 = 8 * tk;
+  float a[8][8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const int r = R0 + u, c = C0 + v;
+      a[u][v] = (r < m && c <= r) ? A[(n0 + r) * ld + n0 + c] : 0.0f;
+    }
+  if (tk == 0) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) col[R0 + u] = a[u][0];
   }
   __syncthreads();
   int first_bad = -1;
   for (int j = 0; j < m; ++j) {
-    const float p = a[j * kLP + j];
-    const float d = sqrtf(p);
+    const float* cj = col + (j & 1) * kNB;
+    const float p = cj[j];
     if (!(p > 0.0f) && first_bad < 0) first_bad = j;
-    if (tid > j && tid < m) a[tid * kLP + j] /= d;
-    __syncthreads();
-    if (tid == 0) a[j * kLP + j] = d;
-    float ar[4], ac[4];
+    const float d = sqrtf(p);
+    const float inv = 1.0f / d;
+    if (R0 + 7 >= j) {
+      float lr[8], lc[8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      ar[u] = a[(4 * ti + u) * kLP + j];
-      ac[u] = a[(4 * tk + u) * kLP + j];
-    }
+      for (int u = 0; u < 8; ++u) lr[u] = (R0 + u > j) ? cj[R0 + u] * inv : 0.0f;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int r = 4 * ti + u;
+      for (int v = 0; v < 8; ++v) lc[v] = (C0 + v > j) ? cj[C0 + v] * inv : 0.0f;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int c = 4 * tk + v;
-        if (r > j && c > j && c <= r) a[r * kLP + c] -= ar[u] * ac[v];
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int v = 0; v < 8; ++v) a[u][v] -= lr[u] * lc[v];
+      if (C0 <= j && j < C0 + 8) {
+        // column j of L: l = a / d below the diagonal, d on it
+#pragma unroll
+        for (int v = 0; v < 8; ++v)
+          if (C0 + v == j) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              const int r = R0 + u;
+              if (r > j) a[u][v] = lr[u];
+              else if (r == j) a[u][v] = d;
+            }
+          }
+      }
+      const int jn = j + 1;
+      if (jn < m && C0 <= jn && jn < C0 + 8) {
+        float* cn = col + (jn & 1) * kNB;
+#pragma unroll
+        for (int v = 0; v < 8; ++v)
+          if (C0 + v == jn) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) cn[R0 + u] = a[u][v];
+          }
       }
     }
     __syncthreads();
   }
   if (first_bad >= 0 && tid == 0) atomicCAS(info, 0, static_cast<int32_t>(n0 + first_bad + 1));
-  // X = L^-1, right-looking: row j of X scaled by 1/L[j][j], then subtracted
-  // from the rows below with weights L[r][j]
-  for (int j = 0; j < m; ++j) {
-    const float dj = a[j * kLP + j];
-    if (tid <= j) x[j * kLP + tid] /= dj;
-    __syncthreads();
-    float lr[4], xc[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      lr[u] = a[(4 * ti + u) * kLP + j];
-      xc[u] = x[j * kLP + 4 * tk + u];
+  for (int u = 0; u < 8; ++u)
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const int r = R0 + u, c = C0 + v;
+      const float val = (c <= r) ? a[u][v] : 0.0f;
+      Ls[r * kLP + c] = val;
+      if (r < m && c < m) A[(n0 + r) * ld + n0 + c] = val;
     }
+  __syncthreads();
+  // X = L^-1, right-looking on rows: row j is scaled by 1/L[j][j] when it is
+  // published, then subtracted from the rows below with weights L[r][j]
+  float x[8][8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int r = 4 * ti + u;
+  for (int u = 0; u < 8; ++u)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int c = 4 * tk + v;
-        if (r > j && r < m && c <= j) x[r * kLP + c] -= lr[u] * xc[v];
+    for (int v = 0; v < 8; ++v) x[u][v] = (R0 + u == C0 + v && R0 + u < m) ? 1.0f : 0.0f;
+  if (ti == 0) {
+    const float s0 = 1.0f / Ls[0];
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      x[0][v] *= s0;
+      xrow[C0 + v] = x[0][v];
+    }
+  }
+  __syncthreads();
+  for (int j = 0; j < m; ++j) {
+    const float* xj = xrow + (j & 1) * kNB;
+    if (R0 + 7 > j) {
+      float lr[8], xc[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) lr[u] = (R0 + u > j) ? Ls[(R0 + u) * kLP + j] : 0.0f;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) xc[v] = xj[C0 + v];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int v = 0; v < 8; ++v) x[u][v] -= lr[u] * xc[v];
+      const int jn = j + 1;
+      if (jn < m && R0 <= jn && jn < R0 + 8) {
+        const float sn = 1.0f / Ls[jn * kLP + jn];
+        float* xn = xrow + (jn & 1) * kNB;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (R0 + u == jn) {
+#pragma unroll
+            for (int v = 0; v < 8; ++v) {
+              x[u][v] *= sn;
+              xn[C0 + v] = x[u][v];
+            }
+          }
       }
     }
     __syncthreads();
   }
-  for (int e = tid; e < kNB * kNB; e += 256) {
-    const int i = e >> 6, j = e & (kNB - 1);
-    if (i >= m || j >= m) continue;
-    A[(n0 + i) * ld + n0 + j] = (j <= i) ? a[i * kLP + j] : 0.0f;
-    X[(n0 + i) * ld + n0 + j] = (j <= i) ? x[i * kLP + j] : 0.0f;
-  }
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const int r = R0 + u, c = C0 + v;
+      if (r < m && c < m) X[(n0 + r) * ld + n0 + c] = (c <= r) ? x[u][v] : 0.0f;
+    }
 }
 
 // in-place U = J X J over the full K x K matrix (swap (i,j) <-> (K-1-i, K-1-j))
@@ -211,7 +273,7 @@ int64_t scratch_floats(int64_t m) {
 int chol_inv(Ctx& c, int64_t n0, int64_t m, float* tmp) {
   const int64_t ld = c.K;
   if (m <= kNB) {
-    hipLaunchKernelGGL(chol_inv_leaf, dim3(1), dim3(256), 2 * kNB * kLP * sizeof(float), c.st, c.A, c.X, ld, n0,
+    hipLaunchKernelGGL(chol_inv_leaf, dim3(1), dim3(256), kLeafLds, c.st, c.A, c.X, ld, n0,
                        static_cast<int>(m), c.info);
     return check_launch("chol_inv_leaf");
   }

@@ -6,10 +6,10 @@
 // z * sum_k x_k) with exact small-integer codes in fp16/bf16 and fp32
 // accumulation, so a code costs one packed decode step and half a v_dot2.
 //
-//  * gemv_m1_k (M = 1): persistent workgroups; x staged once per workgroup in
-//    LDS in the order the packed words decode into fp16/bf16 pairs (one shift
-//    and one and-or per pair), each lane holding the x pairs of its 32-code
-//    chunks in registers across all rows it visits.
+//  * gemv_m1_k (M = 1): persistent workgroups; each lane loads the x values of
+//    its 32-code chunks once, permutes them into the order the packed words
+//    decode into fp16/bf16 pairs (one shift and one and-or per pair) and keeps
+//    them in registers across all rows it visits; no LDS, no barrier.
 //  * gemv_k (M <= 4): 4 waves per workgroup share x staged in LDS; a wave
 //    walks 4 weight rows at a time, lane l taking 128-bit chunks l, l+64, ...
 //    of each row (a wave load covers 1 KiB of contiguous codes).  Within a
@@ -291,20 +291,43 @@ struct Off32 {
   static constexpr float v = BF16 ? Magic<BITS, BF16>::kOffset : 1024.0f;
 };
 
-// M = 1: persistent workgroups of 4 waves; x (pair order) and its 32-chunk
-// sums are staged in LDS once per workgroup, then each lane keeps the x pairs
-// of its chunks in registers for every row it visits.  WS = 1: every wave
-// walks its own rows, lane l taking chunks l, l + 64, ...; WS = 4 (long rows):
-// the four waves share each row, thread t taking chunks t, t + 256, ..., and
-// the partial sums meet in LDS.
+// x pairs of one 32-code chunk, in the chunk's pair order, and their sum:
+// loaded in natural order (64 bytes) and permuted in registers.
+template <int BITS, bool BF16>
+__device__ __forceinline__ void load_x_chunk(const uint16_t* __restrict__ x, int c, uint32_t (&xr)[16], float& xsum) {
+  uint32_t d[16];
+  const u32x4* src = reinterpret_cast<const u32x4*>(x + static_cast<int64_t>(c) * 32);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const u32x4 t = src[v];
+    d[4 * v] = t[0]; d[4 * v + 1] = t[1]; d[4 * v + 2] = t[2]; d[4 * v + 3] = t[3];
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    s += BF16 ? bf16_bits_to_f32(d[q] & 0xffffu) : f16_bits_to_f32(d[q] & 0xffffu);
+    s += BF16 ? bf16_bits_to_f32(d[q] >> 16) : f16_bits_to_f32(d[q] >> 16);
+  }
+  xsum = s;
+#pragma unroll
+  for (int p = 0; p < 16; ++p) {
+    const int ia = pair_a<BITS>(p), ib = pair_b<BITS>(p);
+    const uint32_t lo = (d[ia >> 1] >> (16 * (ia & 1))) & 0xffffu;
+    const uint32_t hi = (d[ib >> 1] >> (16 * (ib & 1))) & 0xffffu;
+    xr[p] = lo | (hi << 16);
+  }
+}
+
+// M = 1: each lane holds the x pairs of its 32-code chunks in registers
+// (loaded straight from x, no LDS staging, no barrier) and streams RB weight
+// rows at a time.  WS = 1: every wave walks its own rows, lane l taking
+// chunks l, l + 64, ...; WS = 4 (long rows): the four waves of a workgroup
+// share each row, thread t taking chunks t, t + 256, ..., and the partial
+// sums meet in LDS.
 template <int BITS, bool BF16, int MAXC, int RB, int WS>
 __global__ __launch_bounds__(256) void gemv_m1_k(LinArgs a) {
-  extern __shared__ uint32_t lds[];
   __shared__ float red[2][4][RB];
-  const int64_t K = a.K;
-  const int nch = static_cast<int>(K / 32);
-  uint32_t* xp_lds = lds;                                   // nch x 16 pair words
-  float* xs_lds = reinterpret_cast<float*>(lds + nch * 16);  // nch sums
+  const int nch = static_cast<int>(a.K / 32);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -314,12 +337,26 @@ __global__ __launch_bounds__(256) void gemv_m1_k(LinArgs a) {
   const int64_t step = WS == 4 ? gridDim.x : static_cast<int64_t>(gridDim.x) * 4;
   int64_t rb = WS == 4 ? blockIdx.x : blockIdx.x * 4LL + wave;
 
-  // the weight stream does not depend on x: start the first batch's loads
-  // before x is staged
-  uint32_t dwA[RB][MAXC][BITS], dwB[RB][MAXC][BITS];
-  float sA[RB][MAXC], zA[RB][MAXC], sB[RB][MAXC], zB[RB][MAXC];
-  auto load_batch = [&](int64_t b, uint32_t (&dw)[RB][MAXC][BITS], float (&sc)[RB][MAXC], float (&zc)[RB][MAXC]) {
-    const int64_t n0 = b * RB;
+  uint32_t xr[MAXC][16];
+  float xsr[MAXC];
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = me + kStride * i;
+    if (c < nch) {
+      load_x_chunk<BITS, BF16>(a.x, c, xr[i], xsr[i]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) xr[i][e] = 0u;
+      xsr[i] = 0.0f;
+    }
+  }
+
+  constexpr float off = Off32<BITS, BF16>::v;
+  int parity = 0;
+  for (; rb < nbatches; rb += step) {
+    const int64_t n0 = rb * RB;
+    uint32_t dw[RB][MAXC][BITS];
+    float sc[RB][MAXC], zc[RB][MAXC];
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
       const int64_t n = std::min<int64_t>(n0 + r, a.N - 1);
@@ -346,60 +383,6 @@ __global__ __launch_bounds__(256) void gemv_m1_k(LinArgs a) {
         zc[r][i] = load_elem(a.zeros, n * a.ngroups + g, a.sz_dtype);
       }
     }
-  };
-  if (rb < nbatches) load_batch(rb, dwA, sA, zA);
-
-  for (int c = tid; c < nch; c += 256) {
-    uint16_t xv[32];
-    const u32x4* src = reinterpret_cast<const u32x4*>(a.x + static_cast<int64_t>(c) * 32);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const u32x4 t = src[v];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        xv[8 * v + 2 * e] = static_cast<uint16_t>(t[e] & 0xffffu);
-        xv[8 * v + 2 * e + 1] = static_cast<uint16_t>(t[e] >> 16);
-      }
-    }
-    float sum = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) sum += BF16 ? bf16_bits_to_f32(xv[e]) : f16_bits_to_f32(xv[e]);
-    u32x4 o[4];
-#pragma unroll
-    for (int p = 0; p < 16; ++p)
-      o[p / 4][p % 4] = static_cast<uint32_t>(xv[pair_a<BITS>(p)]) | (static_cast<uint32_t>(xv[pair_b<BITS>(p)]) << 16);
-    u32x4* dst = reinterpret_cast<u32x4*>(xp_lds + c * 16);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) dst[v] = o[v];
-    xs_lds[c] = sum;
-  }
-  __syncthreads();
-
-  uint32_t xr[MAXC][16];
-  float xsr[MAXC];
-#pragma unroll
-  for (int i = 0; i < MAXC; ++i) {
-    const int c = me + kStride * i;
-    if (c < nch) {
-      const u32x4* srcv = reinterpret_cast<const u32x4*>(xp_lds + c * 16);
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const u32x4 t = srcv[v];
-        xr[i][4 * v] = t[0]; xr[i][4 * v + 1] = t[1]; xr[i][4 * v + 2] = t[2]; xr[i][4 * v + 3] = t[3];
-      }
-      xsr[i] = xs_lds[c];
-    } else {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) xr[i][e] = 0u;
-      xsr[i] = 0.0f;
-    }
-  }
-
-  constexpr float off = Off32<BITS, BF16>::v;
-  int parity = 0;
-  auto compute = [&](int64_t b, const uint32_t (&dw)[RB][MAXC][BITS], const float (&sc)[RB][MAXC],
-                     const float (&zc)[RB][MAXC]) {
-    const int64_t n0 = b * RB;
     float acc[RB];
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
@@ -434,18 +417,6 @@ __global__ __launch_bounds__(256) void gemv_m1_k(LinArgs a) {
         store_elem(a.y, n, a.y_dtype, acc[r] + bias);
       }
     }
-  };
-
-  // double-buffered walk over this wave's (or workgroup's) row batches
-  while (rb < nbatches) {
-    const int64_t nb1 = rb + step;
-    if (nb1 < nbatches) load_batch(nb1, dwB, sB, zB);
-    compute(rb, dwA, sA, zA);
-    if (nb1 >= nbatches) break;
-    const int64_t nb2 = nb1 + step;
-    if (nb2 < nbatches) load_batch(nb2, dwA, sA, zA);
-    compute(nb1, dwB, sB, zB);
-    rb = nb2;
   }
 }
 
@@ -636,8 +607,7 @@ int launch_m1(hipStream_t st, const LinArgs& a) {
   const int64_t nbatches = cdiv(a.N, RB);
   const int64_t per_wg = WS == 4 ? 1 : 4;
   const unsigned blocks = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(cdiv(nbatches, per_wg), 1024)));
-  const size_t lds = static_cast<size_t>(a.K / 32) * (16 * 4 + 4);
-  hipLaunchKernelGGL((gemv_m1_k<BITS, BF16, MAXC, RB, WS>), dim3(blocks), dim3(256), lds, st, a);
+  hipLaunchKernelGGL((gemv_m1_k<BITS, BF16, MAXC, RB, WS>), dim3(blocks), dim3(256), 0, st, a);
   return check_launch("gemv_m1");
 }
 
@@ -645,7 +615,8 @@ template <int BITS, bool BF16>
 int launch_fast(hipStream_t st, const LinArgs& a) {
   using F = Fmt<BITS>;
   const int64_t nch = a.K / F::CB;
-  if (a.M == 1 && a.K % 32 == 0 && a.gs % 32 == 0 && a.K <= 4 * 256 * 32) {
+  if (a.M == 1 && a.K % 32 == 0 && a.gs % 32 == 0 && a.K <= 4 * 256 * 32 &&
+      (reinterpret_cast<uintptr_t>(a.x) % 16) == 0) {
     const int64_t nch32 = a.K / 32;
     if (nch32 <= 64) return launch_m1<BITS, BF16, 1, 1>(st, a);
     if (nch32 <= 128) return launch_m1<BITS, BF16, 2, 1>(st, a);
