@@ -232,10 +232,18 @@ __global__ __launch_bounds__(256) void gemv_k(LinArgs a) {
   }
 }
 
-// -------------------------------------------------------- M = 1 GEMV v2 --
+// ------------------------------------------------------------ M = 1 GEMV --
 // 32-code chunks for every width (BITS dwords per chunk).  Pair p of a chunk
-// holds the codes (pair_a(p), pair_b(p)) -- the pairing one shift and one
-// and-or extract from the packed words -- and x is staged in the same order.
+// holds the codes (pair_a(p), pair_b(p)): the two codes one and-or lifts out
+// of a packed dword into the low and high halves, under the fp16 magic
+// exponent 0x6400 (value 1024 + code) or the bf16 one 0x4300 (128 + code).
+// With fp16, a mask need not sit at bit 0: (w & 0x00F000F0) | 0x64006400 is
+// 1024 + 16 * code, exact, so 4-bit pairs need one shift per dword and 2-bit
+// pairs one per dword too; pairs then fall into "classes" by the power of
+// two m_c their codes carry, each with its own accumulator, and
+//   sum_k x_k (q_k - z) = sum_c acc_c / m_c - sum_c (off / m_c + z) X_c
+// where X_c sums the x values of class c.  The x pairs are stored in the
+// same order as the pairs, so each costs one and-or and one v_dot2.
 template <int BITS>
 __host__ __device__ constexpr int pair_a(int p) {
   return BITS == 4 ? 8 * (p / 4) + p % 4 : BITS == 2 ? 16 * (p / 8) + p % 8 : BITS == 8 ? 4 * (p / 2) + p % 2 : p;
@@ -245,70 +253,83 @@ __host__ __device__ constexpr int pair_b(int p) {
   return pair_a<BITS>(p) + (BITS == 4 ? 4 : BITS == 2 ? 8 : BITS == 8 ? 2 : 16);
 }
 
-template <int BITS, int P>
-__device__ __forceinline__ uint32_t pair32(const uint32_t* dw) {
+template <int BITS, bool BF16>
+struct M1Fmt {
+  // scale classes: fp16 4-bit pairs alternate x1 / x16; fp16 2-bit cycle x1 x4 x16 x64
+  static constexpr int NCLS = BF16 ? 1 : BITS == 4 ? 2 : BITS == 2 ? 4 : 1;
+  static constexpr float kOff = BF16 ? (BITS == 8 ? 0.0f : 128.0f) : 1024.0f;
+  static constexpr int cls(int p) { return p % NCLS; }
+  static constexpr float mult(int c) { return static_cast<float>(1 << (BITS * c)); }
+};
+
+// pair P of the chunk with the magic exponent already or-ed in
+template <int BITS, bool BF16, int P>
+__device__ __forceinline__ uint32_t m1_pair(const uint32_t* dw, uint32_t magic) {
   if constexpr (BITS == 4) {
-    return (dw[P / 4] >> (4 * (P % 4))) & 0x000F000Fu;
+    constexpr int d = P / 4, i = P % 4;
+    if constexpr (!BF16) {
+      const uint32_t w = (i >= 2) ? (dw[d] >> 8) : dw[d];
+      return (w & (0x000F000Fu << (4 * (i & 1)))) | magic;
+    } else {
+      return ((dw[d] >> (4 * i)) & 0x000F000Fu) | magic;
+    }
   } else if constexpr (BITS == 2) {
-    return (dw[P / 8] >> (2 * (P % 8))) & 0x00030003u;
+    constexpr int d = P / 8, i = P % 8;
+    if constexpr (!BF16) {
+      const uint32_t w = (i >= 4) ? (dw[d] >> 8) : dw[d];
+      return (w & (0x00030003u << (2 * (i & 3)))) | magic;
+    } else {
+      return ((dw[d] >> (2 * i)) & 0x00030003u) | magic;
+    }
   } else if constexpr (BITS == 8) {
-    return (dw[P / 2] >> (8 * (P % 2))) & 0x00FF00FFu;
+    constexpr int d = P / 2, i = P % 2;
+    const uint32_t w = dw[d] >> (8 * i);
+    if constexpr (!BF16) return (w & 0x00FF00FFu) | magic;
+    else return bf16_pair_exact(w & 0x00FF00FFu);
   } else {
-    constexpr int b0 = 3 * P, b1 = 3 * P + 48;
+    // 3-bit: code P at bit 3P, code P + 16 at bit 3P + 48 (funnel shifts)
+    constexpr int b0 = 3 * P, b1 = 3 * P + 32;
     constexpr int d0 = b0 / 32, o0 = b0 % 32, d1 = b1 / 32, o1 = b1 % 32;
-    uint32_t lo = dw[d0] >> o0;
-    if constexpr (o0 > 29 && d0 + 1 < 3) lo |= dw[d0 + 1] << (32 - o0);
-    uint32_t hi = dw[d1] >> o1;
-    if constexpr (o1 > 29 && d1 + 1 < 3) hi |= dw[d1 + 1] << (32 - o1);
-    return (lo & 7u) | ((hi & 7u) << 16);
+    const uint32_t lo = (o0 == 0 || d0 + 1 >= 3) ? (dw[d0] >> o0) : __builtin_amdgcn_alignbit(dw[d0 + 1], dw[d0], o0);
+    const uint32_t hi = (o1 == 0 || d1 + 1 >= 3) ? (dw[d1] >> o1) : __builtin_amdgcn_alignbit(dw[d1 + 1], dw[d1], o1);
+    return (lo & 7u) | (hi & 0x70000u) | magic;
   }
 }
 
-// sum over the chunk of x * (code + offset): offset 1024 (fp16) or 128 (bf16,
-// widths < 8), 0 for 8-bit bf16 codes (converted exactly)
-template <int BITS, bool BF16, int P>
-__device__ __forceinline__ float dot_pair32(const uint32_t* dw, uint32_t xpair, float acc) {
-  const uint32_t c = pair32<BITS, P>(dw);
-  if constexpr (!BF16) {
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, c | 0x64006400u), __builtin_bit_cast(f16x2, xpair), acc,
-                                  false);
-  } else {
-    const uint32_t t = Magic<BITS, BF16>::kBF16Offset ? (c | 0x43004300u) : bf16_pair_exact(c);
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, t), __builtin_bit_cast(bf16x2, xpair), acc,
-                                           false);
-  }
+template <bool BF16>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+  if constexpr (BF16)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), acc, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), acc, false);
 }
 
 template <int BITS, bool BF16, int... Ps>
-__device__ __forceinline__ float dot_chunk32(const uint32_t* dw, const uint32_t* xp, std::integer_sequence<int, Ps...>) {
-  float acc = 0.0f;
-  ((acc = dot_pair32<BITS, BF16, Ps>(dw, xp[Ps], acc)), ...);
-  return acc;
+__device__ __forceinline__ void m1_dot(const uint32_t* dw, const uint32_t* xp, uint32_t magic,
+                                       float (&acc)[M1Fmt<BITS, BF16>::NCLS], std::integer_sequence<int, Ps...>) {
+  using F = M1Fmt<BITS, BF16>;
+#pragma unroll
+  for (int c = 0; c < F::NCLS; ++c) acc[c] = 0.0f;
+  ((acc[F::cls(Ps)] = dot2<BF16>(m1_pair<BITS, BF16, Ps>(dw, magic), xp[Ps], acc[F::cls(Ps)])), ...);
 }
 
-template <int BITS, bool BF16>
-struct Off32 {
-  static constexpr float v = BF16 ? Magic<BITS, BF16>::kOffset : 1024.0f;
-};
-
-// x pairs of one 32-code chunk, in the chunk's pair order, and their sum:
-// loaded in natural order (64 bytes) and permuted in registers.
-template <int BITS, bool BF16>
-__device__ __forceinline__ void load_x_chunk(const uint16_t* __restrict__ x, int c, uint32_t (&xr)[16], float& xsum) {
-  uint32_t d[16];
+// natural-order x of one 32-code chunk (64 bytes)
+__device__ __forceinline__ void load_x_raw(const uint16_t* __restrict__ x, int c, u32x4 (&raw)[4]) {
   const u32x4* src = reinterpret_cast<const u32x4*>(x + static_cast<int64_t>(c) * 32);
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const u32x4 t = src[v];
-    d[4 * v] = t[0]; d[4 * v + 1] = t[1]; d[4 * v + 2] = t[2]; d[4 * v + 3] = t[3];
-  }
-  float s = 0.0f;
+  for (int v = 0; v < 4; ++v) raw[v] = src[v];
+}
+
+// x pairs of one 32-code chunk in pair order, their total X and the magic
+// correction Y = sum_c (off / m_c) X_c
+template <int BITS, bool BF16>
+__device__ __forceinline__ void prep_x_chunk(const u32x4 (&raw)[4], uint32_t (&xr)[16], float& xs, float& ys) {
+  using F = M1Fmt<BITS, BF16>;
+  uint32_t d[16];
 #pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    s += BF16 ? bf16_bits_to_f32(d[q] & 0xffffu) : f16_bits_to_f32(d[q] & 0xffffu);
-    s += BF16 ? bf16_bits_to_f32(d[q] >> 16) : f16_bits_to_f32(d[q] >> 16);
+  for (int v = 0; v < 4; ++v) {
+    d[4 * v] = raw[v][0]; d[4 * v + 1] = raw[v][1]; d[4 * v + 2] = raw[v][2]; d[4 * v + 3] = raw[v][3];
   }
-  xsum = s;
 #pragma unroll
   for (int p = 0; p < 16; ++p) {
     const int ia = pair_a<BITS>(p), ib = pair_b<BITS>(p);
@@ -316,87 +337,200 @@ __device__ __forceinline__ void load_x_chunk(const uint16_t* __restrict__ x, int
     const uint32_t hi = (d[ib >> 1] >> (16 * (ib & 1))) & 0xffffu;
     xr[p] = lo | (hi << 16);
   }
+  const uint32_t one = BF16 ? 0x3F803F80u : 0x3C003C00u;
+  float cs[F::NCLS];
+#pragma unroll
+  for (int c = 0; c < F::NCLS; ++c) cs[c] = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 16; ++p) cs[F::cls(p)] = dot2<BF16>(xr[p], one, cs[F::cls(p)]);
+  xs = 0.0f;
+  ys = 0.0f;
+#pragma unroll
+  for (int c = 0; c < F::NCLS; ++c) {
+    xs += cs[c];
+    ys += (F::kOff / F::mult(c)) * cs[c];
+  }
 }
 
-// M = 1: each lane holds the x pairs of its 32-code chunks in registers
-// (loaded straight from x, no LDS staging, no barrier) and streams RB weight
-// rows at a time.  WS = 1: every wave walks its own rows, lane l taking
-// chunks l, l + 64, ...; WS = 4 (long rows): the four waves of a workgroup
-// share each row, thread t taking chunks t, t + 256, ..., and the partial
-// sums meet in LDS.
-template <int BITS, bool BF16, int MAXC, int RB, int WS>
+constexpr int kBufDword3 = 0x00020000;  // raw buffer descriptor word 3 (gfx950)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                           kBufDword3);
+}
+
+// codes, scales and zeros of RB rows x MAXC chunks of one lane
+template <int BITS, int MAXC, int RB>
+struct M1Batch {
+  uint32_t dw[RB][MAXC][BITS];
+  uint16_t s[RB][MAXC], z[RB][MAXC];
+  uint32_t b32;  // lane r < RB: bias of row n0 + r when the bias is fp32
+  uint16_t b16;  // ... when it is 16-bit
+};
+
+// Each row is addressed through its own buffer descriptors (wave-uniform,
+// scalar registers) and a lane's chunk offsets are loop-invariant vector
+// registers, so a load costs no address arithmetic.  Rows at or beyond N get
+// empty descriptors: their loads return zeros and touch no memory.
+template <int BITS, int MAXC, int RB>
+__device__ __forceinline__ void load_m1_batch(const LinArgs& a, int64_t n0, const uint32_t (&coff)[MAXC],
+                                              const uint32_t (&goff)[MAXC], M1Batch<BITS, MAXC, RB>& b) {
+  const uint16_t* sc = static_cast<const uint16_t*>(a.scales);
+  const uint16_t* zr = static_cast<const uint16_t*>(a.zeros);
+  {
+    // bias of the batch's rows, one per lane, issued with the batch (never
+    // behind a later prefetch): the descriptor of the other width is empty
+    const int lane = threadIdx.x & 63;
+    const int64_t left = n0 < a.N ? std::min<int64_t>(a.N - n0, RB) : 0;
+    const bool f32 = a.bias_dtype == GPTQ_F32;
+    const uint32_t n32 = a.bias && f32 ? static_cast<uint32_t>(left * 4) : 0u;
+    const uint32_t n16 = a.bias && !f32 ? static_cast<uint32_t>(left * 2) : 0u;
+    const char* bb = static_cast<const char*>(a.bias);
+    const uint32_t ln = static_cast<uint32_t>(lane < RB ? lane : RB);
+    b.b32 = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(bb + n0 * 4, n32), ln * 4, 0, 0);
+    b.b16 = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(bb + n0 * 2, n16), ln * 2, 0, 0);
+  }
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const int64_t n = n0 + r;
+    const bool ok = n < a.N;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.packed + n * a.pitch, ok ? static_cast<uint32_t>(a.pitch) : 0u);
+    const uint32_t gb = ok ? static_cast<uint32_t>(a.ngroups * 2) : 0u;
+    const __amdgpu_buffer_rsrc_t srs = make_rsrc(sc + n * a.ngroups, gb);
+    const __amdgpu_buffer_rsrc_t zrs = make_rsrc(zr + n * a.ngroups, gb);
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) {
+      if constexpr (BITS % 4 == 0) {
+#pragma unroll
+        for (int v = 0; v < BITS / 4; ++v) {
+          const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(wr, coff[i] + 16 * v, 0, 2);
+          b.dw[r][i][4 * v] = t[0]; b.dw[r][i][4 * v + 1] = t[1];
+          b.dw[r][i][4 * v + 2] = t[2]; b.dw[r][i][4 * v + 3] = t[3];
+        }
+      } else if constexpr (BITS == 2) {
+        const u32x2 t = __builtin_amdgcn_raw_buffer_load_b64(wr, coff[i], 0, 2);
+        b.dw[r][i][0] = t[0]; b.dw[r][i][1] = t[1];
+      } else {
+        typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+        const u32x3 t = __builtin_amdgcn_raw_buffer_load_b96(wr, coff[i], 0, 2);
+        b.dw[r][i][0] = t[0]; b.dw[r][i][1] = t[1]; b.dw[r][i][2] = t[2];
+      }
+      b.s[r][i] = __builtin_amdgcn_raw_buffer_load_b16(srs, goff[i], 0, 0);
+      b.z[r][i] = __builtin_amdgcn_raw_buffer_load_b16(zrs, goff[i], 0, 0);
+    }
+  }
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// sum over the 64 lanes, returned wave-uniform: butterflies inside each row
+// of 16 lanes (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror),
+// then the four row totals read from lanes 0, 16, 32, 48
+__device__ __forceinline__ float wave_total(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x141>(v);
+  v += dpp_mov<0x140>(v);
+  const int b = __builtin_bit_cast(int, v);
+  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
+         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
+}
+
+// a 16-bit scale or zero: bf16 when SZBF, else fp16
+template <bool SZBF>
+__device__ __forceinline__ float sz_val(uint16_t b) {
+  return SZBF ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+}
+
+template <int BITS, bool BF16, bool SZBF, int MAXC, int RB>
+__device__ __forceinline__ void m1_rows(const M1Batch<BITS, MAXC, RB>& b, const uint32_t (&xr)[MAXC][16],
+                                        const float (&xsr)[MAXC], const float (&ysr)[MAXC], uint32_t magic,
+                                        bool bias_bf, float (&acc)[RB], float& bias) {
+  bias = __uint_as_float(b.b32) + (bias_bf ? bf16_bits_to_f32(b.b16) : f16_bits_to_f32(b.b16));
+  using F = M1Fmt<BITS, BF16>;
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    float sacc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) {
+      float cacc[F::NCLS];
+      m1_dot<BITS, BF16>(b.dw[r][i], xr[i], magic, cacc, std::make_integer_sequence<int, 16>{});
+      float t = cacc[0];
+#pragma unroll
+      for (int c = 1; c < F::NCLS; ++c) t += cacc[c] * (1.0f / F::mult(c));
+      t -= ysr[i];
+      t -= sz_val<SZBF>(b.z[r][i]) * xsr[i];
+      sacc += sz_val<SZBF>(b.s[r][i]) * t;
+    }
+    acc[r] = sacc;
+  }
+  // reductions after all rows, so that the rows' DPP chains interleave
+#pragma unroll
+  for (int r = 0; r < RB; ++r) acc[r] = wave_total(acc[r]);
+}
+
+// M = 1 (16-bit scales/zeros).  Each lane holds the x pairs of its 32-code
+// chunks in registers and streams RB weight rows at a time.  WS = 1: every
+// wave walks its own rows, lane l taking chunks l, l + 64, ...; WS = 4 (long
+// rows): the four waves of a workgroup share each row, thread t taking chunks
+// t, t + 256, ..., and the row totals meet in LDS.  Lanes past the last chunk
+// hold zero x and read zeros.  Batches are double-buffered: the next batch's
+// loads are issued before the current one is reduced.
+template <int BITS, bool BF16, bool SZBF, int MAXC, int RB, int WS>
 __global__ __launch_bounds__(256) void gemv_m1_k(LinArgs a) {
   __shared__ float red[2][4][RB];
   const int nch = static_cast<int>(a.K / 32);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int me = WS == 4 ? tid : lane;
   constexpr int kStride = 64 * WS;
   const int64_t nbatches = cdiv(a.N, RB);
   const int64_t step = WS == 4 ? gridDim.x : static_cast<int64_t>(gridDim.x) * 4;
   int64_t rb = WS == 4 ? blockIdx.x : blockIdx.x * 4LL + wave;
+  if (rb >= nbatches) return;
+  const int cpg = a.gs / 32;  // chunks per group
 
-  uint32_t xr[MAXC][16];
-  float xsr[MAXC];
+  uint32_t coff[MAXC], goff[MAXC];
+  int cidx[MAXC];
 #pragma unroll
   for (int i = 0; i < MAXC; ++i) {
     const int c = me + kStride * i;
-    if (c < nch) {
-      load_x_chunk<BITS, BF16>(a.x, c, xr[i], xsr[i]);
-    } else {
+    const bool ok = c < nch;
+    cidx[i] = ok ? c : nch - 1;
+    coff[i] = ok ? static_cast<uint32_t>(c) * (4 * BITS) : static_cast<uint32_t>(a.pitch);      // out of range -> 0
+    goff[i] = ok ? static_cast<uint32_t>(c / cpg) * 2 : static_cast<uint32_t>(a.ngroups * 2);  // out of range -> 0
+  }
+  u32x4 xraw[MAXC][4];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) xr[i][e] = 0u;
-      xsr[i] = 0.0f;
+  for (int i = 0; i < MAXC; ++i) load_x_raw(a.x, cidx[i], xraw[i]);
+  M1Batch<BITS, MAXC, RB> A, B;
+  load_m1_batch<BITS, MAXC, RB>(a, rb * RB, coff, goff, A);
+
+  uint32_t xr[MAXC][16];
+  float xsr[MAXC], ysr[MAXC];
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    prep_x_chunk<BITS, BF16>(xraw[i], xr[i], xsr[i], ysr[i]);
+    if (me + kStride * i >= nch) {
+#pragma unroll
+      for (int p = 0; p < 16; ++p) xr[i][p] = 0u;
+      xsr[i] = ysr[i] = 0.0f;
     }
   }
+  // the magic exponent lives in a vector register so that mask-and-or is one v_and_or_b32
+  uint32_t magic;
+  if constexpr (BF16) asm("v_mov_b32 %0, 0x43004300" : "=v"(magic));
+  else asm("v_mov_b32 %0, 0x64006400" : "=v"(magic));
 
-  constexpr float off = Off32<BITS, BF16>::v;
   int parity = 0;
-  for (; rb < nbatches; rb += step) {
-    const int64_t n0 = rb * RB;
-    uint32_t dw[RB][MAXC][BITS];
-    float sc[RB][MAXC], zc[RB][MAXC];
-#pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      const int64_t n = std::min<int64_t>(n0 + r, a.N - 1);
-      const uint8_t* row = a.packed + n * a.pitch;
-#pragma unroll
-      for (int i = 0; i < MAXC; ++i) {
-        const int c = std::min(me + kStride * i, nch - 1);
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(row + static_cast<int64_t>(c) * (4 * BITS));
-        if constexpr (BITS % 4 == 0) {
-#pragma unroll
-          for (int v = 0; v < BITS / 4; ++v) {
-            const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + v);
-            dw[r][i][4 * v] = t[0]; dw[r][i][4 * v + 1] = t[1]; dw[r][i][4 * v + 2] = t[2]; dw[r][i][4 * v + 3] = t[3];
-          }
-        } else if constexpr (BITS == 2) {
-          const u32x2 t = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src));
-          dw[r][i][0] = t[0]; dw[r][i][1] = t[1];
-        } else {
-#pragma unroll
-          for (int v = 0; v < 3; ++v) dw[r][i][v] = __builtin_nontemporal_load(src + v);
-        }
-        const int64_t g = (static_cast<int64_t>(c) * 32) / a.gs;
-        sc[r][i] = load_elem(a.scales, n * a.ngroups + g, a.sz_dtype);
-        zc[r][i] = load_elem(a.zeros, n * a.ngroups + g, a.sz_dtype);
-      }
-    }
-    float acc[RB];
-#pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      float sacc = 0.0f;
-#pragma unroll
-      for (int i = 0; i < MAXC; ++i) {
-        const int c = me + kStride * i;
-        if (c < nch) {
-          const float d = dot_chunk32<BITS, BF16>(dw[r][i], xr[i], std::make_integer_sequence<int, 16>{});
-          sacc += sc[r][i] * (d - (zc[r][i] + off) * xsr[i]);
-        }
-      }
-      acc[r] = wave_sum(sacc);
-    }
+  const bool bias_bf = a.bias_dtype == GPTQ_BF16;
+  auto finish = [&](float (&acc)[RB], float bias, int64_t n0) {
     if constexpr (WS == 4) {
       if (lane == 0) {
 #pragma unroll
@@ -405,18 +539,37 @@ __global__ __launch_bounds__(256) void gemv_m1_k(LinArgs a) {
       __syncthreads();
 #pragma unroll
       for (int r = 0; r < RB; ++r)
-        acc[r] = red[parity][0][r] + red[parity][1][r] + red[parity][2][r] + red[parity][3][r];
+        acc[r] = (red[parity][0][r] + red[parity][1][r]) + (red[parity][2][r] + red[parity][3][r]);
       parity ^= 1;
     }
-    if (lane == 0 && (WS == 1 || wave == 0)) {
+    // lane r holds row r's bias: read it out while every lane is active
+    float bv[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) bv[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bias), r));
+    if ((WS == 1 || wave == 0) && lane == 0) {
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
         const int64_t n = n0 + r;
-        if (n >= a.N) continue;
-        const float bias = a.bias ? load_elem(a.bias, n, a.bias_dtype) : 0.0f;
-        store_elem(a.y, n, a.y_dtype, acc[r] + bias);
+        if (n >= a.N) break;
+        const float v = acc[r] + bv[r];
+        a.y[n] = BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
       }
     }
+  };
+  for (;;) {
+    float acc[RB], bias;
+    load_m1_batch<BITS, MAXC, RB>(a, (rb + step) * RB, coff, goff, B);
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
+    m1_rows<BITS, BF16, SZBF, MAXC, RB>(A, xr, xsr, ysr, magic, bias_bf, acc, bias);
+    finish(acc, bias, rb * RB);
+    rb += step;
+    if (rb >= nbatches) break;
+    load_m1_batch<BITS, MAXC, RB>(a, (rb + step) * RB, coff, goff, A);
+    __builtin_amdgcn_sched_barrier(0);
+    m1_rows<BITS, BF16, SZBF, MAXC, RB>(B, xr, xsr, ysr, magic, bias_bf, acc, bias);
+    finish(acc, bias, rb * RB);
+    rb += step;
+    if (rb >= nbatches) break;
   }
 }
 
@@ -601,27 +754,46 @@ __global__ __launch_bounds__(256) void linear_generic(const void* __restrict__ x
   }
 }
 
-template <int BITS, bool BF16, int MAXC, int WS>
+template <int BITS, bool BF16, bool SZBF, int MAXC, int WS>
 int launch_m1(hipStream_t st, const LinArgs& a) {
-  constexpr int RB = BITS == 8 ? (MAXC >= 2 ? 2 : 4) : (MAXC >= 2 ? 4 : 8);
+  // rows per batch: at most 16 code dwords per lane and buffer (measured best on MI355X)
+  constexpr int kBudget = 16;
+  constexpr int kFit = kBudget / (MAXC * BITS) > 0 ? kBudget / (MAXC * BITS) : 1;
+  constexpr int RB = kFit >= 8 ? 8 : kFit >= 4 ? 4 : kFit >= 2 ? 2 : 1;
   const int64_t nbatches = cdiv(a.N, RB);
   const int64_t per_wg = WS == 4 ? 1 : 4;
-  const unsigned blocks = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(cdiv(nbatches, per_wg), 1024)));
-  hipLaunchKernelGGL((gemv_m1_k<BITS, BF16, MAXC, RB, WS>), dim3(blocks), dim3(256), 0, st, a);
+  const unsigned blocks = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(cdiv(nbatches, per_wg), 512)));
+  hipLaunchKernelGGL((gemv_m1_k<BITS, BF16, SZBF, MAXC, RB, WS>), dim3(blocks), dim3(256), 0, st, a);
   return check_launch("gemv_m1");
+}
+
+template <int BITS, bool BF16, bool SZBF>
+int launch_m1_k(hipStream_t st, const LinArgs& a) {
+  const int64_t nch32 = a.K / 32;
+  if (nch32 <= 64) return launch_m1<BITS, BF16, SZBF, 1, 1>(st, a);
+  if (nch32 <= 128) return launch_m1<BITS, BF16, SZBF, 2, 1>(st, a);
+  if (nch32 <= 512) return launch_m1<BITS, BF16, SZBF, 2, 4>(st, a);
+  return launch_m1<BITS, BF16, SZBF, 4, 4>(st, a);
+}
+
+// fp16 scales with either activation type; bf16 scales with bf16 activations
+template <int BITS, bool BF16>
+int launch_m1_sz(hipStream_t st, const LinArgs& a) {
+  if constexpr (BF16) {
+    if (a.sz_dtype == GPTQ_BF16) return launch_m1_k<BITS, true, true>(st, a);
+  }
+  return launch_m1_k<BITS, BF16, false>(st, a);
 }
 
 template <int BITS, bool BF16>
 int launch_fast(hipStream_t st, const LinArgs& a) {
   using F = Fmt<BITS>;
   const int64_t nch = a.K / F::CB;
+  // buffer descriptors address a row (pitch bytes) and the scale/zero arrays with 31-bit offsets
   if (a.M == 1 && a.K % 32 == 0 && a.gs % 32 == 0 && a.K <= 4 * 256 * 32 &&
-      (reinterpret_cast<uintptr_t>(a.x) % 16) == 0) {
-    const int64_t nch32 = a.K / 32;
-    if (nch32 <= 64) return launch_m1<BITS, BF16, 1, 1>(st, a);
-    if (nch32 <= 128) return launch_m1<BITS, BF16, 2, 1>(st, a);
-    if (nch32 <= 512) return launch_m1<BITS, BF16, 2, 4>(st, a);
-    return launch_m1<BITS, BF16, 4, 4>(st, a);
+      (a.sz_dtype == GPTQ_F16 || (BF16 && a.sz_dtype == GPTQ_BF16)) &&
+      a.N * a.ngroups * 2 <= INT32_MAX && (reinterpret_cast<uintptr_t>(a.x) % 16) == 0) {
+    return launch_m1_sz<BITS, BF16>(st, a);
   }
   if (a.M <= 4) {
     const size_t lds = static_cast<size_t>(a.M) * a.K * 2 + static_cast<size_t>(a.M) * nch * 4;

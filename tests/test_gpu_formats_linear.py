@@ -55,7 +55,7 @@ def _case(M, N, K, bits, gs, seed, xdt):
     codes = rng.integers(0, 2 ** bits, (N, K)).astype(np.uint8)
     ng = -(-K // gs)
     scales = torch.from_numpy(rng.uniform(1e-3, 1e-2, (N, ng))).half()
-    zeros = torch.full((N, ng), float(2 ** (bits - 1))).half()
+    zeros = torch.from_numpy(rng.integers(0, 2 ** bits, (N, ng)).astype(np.float64)).half()
     x = torch.from_numpy(rng.standard_normal((M, K))).to(xdt)
     return codes, scales, zeros, x
 
@@ -91,6 +91,26 @@ def test_linear_m1_gemv(hip, xdt, bits, K, gs):
     packed = torch.from_numpy(O.pack_bitstream(codes, bits)).cuda()
     y = _ops.linear(x.cuda(), packed, bits, scales.cuda(), zeros.cuda(), K, group_size=gs)
     ref = O.linear(x.float().numpy(), codes, scales.numpy(), zeros.numpy(), np.arange(K) // gs)
+    err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err < TOL[xdt], err
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bits", [3, 4])
+@pytest.mark.parametrize("N,K", [(8192 + 37, 4096), (4096 + 5, 14336), (1024 + 3, 20480)])
+def test_linear_m1_many_rows(hip, xdt, bits, N, K):
+    """M = 1 with more rows than one pass of the grid covers, so every wave
+    walks several double-buffered batches; a ragged last batch, a bias, and
+    scales/zeros in the activation dtype."""
+    from distributed_gptq_amd import _ops
+    gs = 128
+    codes, scales, zeros, x = _case(1, N, K, bits, gs, N + bits, xdt)
+    scales, zeros = scales.to(xdt), zeros.to(xdt)
+    bias = torch.randn(N).to(xdt)
+    packed = torch.from_numpy(O.pack_bitstream(codes, bits)).cuda()
+    y = _ops.linear(x.cuda(), packed, bits, scales.cuda(), zeros.cuda(), K, group_size=gs, bias=bias.cuda())
+    ref = O.linear(x.float().numpy(), codes, scales.float().numpy(), zeros.float().numpy(), np.arange(K) // gs,
+                   bias.float().numpy())
     err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
     assert err < TOL[xdt], err
 
