@@ -123,11 +123,18 @@ __global__ __launch_bounds__(256) void chol_inv_leaf(float* __restrict__ A, floa
     const float d = sqrtf(p);
     const float inv = 1.0f / d;
     if (R0 + 7 >= j) {
+      // unconditional vector reads, masked afterwards (a guarded read would
+      // become a branch with its own LDS round trip)
+      float cr[8], cc[8];
+      *reinterpret_cast<f32x4*>(cr) = *reinterpret_cast<const f32x4*>(cj + R0);
+      *reinterpret_cast<f32x4*>(cr + 4) = *reinterpret_cast<const f32x4*>(cj + R0 + 4);
+      *reinterpret_cast<f32x4*>(cc) = *reinterpret_cast<const f32x4*>(cj + C0);
+      *reinterpret_cast<f32x4*>(cc + 4) = *reinterpret_cast<const f32x4*>(cj + C0 + 4);
       float lr[8], lc[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) lr[u] = (R0 + u > j) ? cj[R0 + u] * inv : 0.0f;
+      for (int u = 0; u < 8; ++u) lr[u] = (R0 + u > j) ? cr[u] * inv : 0.0f;
 #pragma unroll
-      for (int v = 0; v < 8; ++v) lc[v] = (C0 + v > j) ? cj[C0 + v] * inv : 0.0f;
+      for (int v = 0; v < 8; ++v) lc[v] = (C0 + v > j) ? cc[v] * inv : 0.0f;
 #pragma unroll
       for (int u = 0; u < 8; ++u)
 #pragma unroll
@@ -188,11 +195,13 @@ __global__ __launch_bounds__(256) void chol_inv_leaf(float* __restrict__ A, floa
   for (int j = 0; j < m; ++j) {
     const float* xj = xrow + (j & 1) * kNB;
     if (R0 + 7 > j) {
-      float lr[8], xc[8];
+      float lt[8], lr[8], xc[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) lr[u] = (R0 + u > j) ? Ls[(R0 + u) * kLP + j] : 0.0f;
+      for (int u = 0; u < 8; ++u) lt[u] = Ls[(R0 + u) * kLP + j];
+      *reinterpret_cast<f32x4*>(xc) = *reinterpret_cast<const f32x4*>(xj + C0);
+      *reinterpret_cast<f32x4*>(xc + 4) = *reinterpret_cast<const f32x4*>(xj + C0 + 4);
 #pragma unroll
-      for (int v = 0; v < 8; ++v) xc[v] = xj[C0 + v];
+      for (int u = 0; u < 8; ++u) lr[u] = (R0 + u > j) ? lt[u] : 0.0f;
 #pragma unroll
       for (int u = 0; u < 8; ++u)
 #pragma unroll

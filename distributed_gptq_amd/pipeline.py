@@ -10,7 +10,11 @@ results.
 
 ``quantize_layers`` takes, per layer, its weight and a key naming its
 Hessian; every device result stays on the GPU and the only host sync is the
-positive-definiteness check at the end.
+positive-definiteness check at the end.  Each Hessian's chain (damping +
+factorisation, then the sweeps of the layers sharing it) is independent of
+the others, and every one of them is a sequence of latency-bound launches, so
+the chains run on separate streams (at most ``streams``; one stream per chain
+of the same device) and overlap on the GPU.
 """
 from __future__ import annotations
 
@@ -47,41 +51,70 @@ def factorize(H: torch.Tensor, nsamples: int, percdamp: float, actorder: bool):
     return U, perm, dead, info
 
 
+_SIDE_STREAMS: Dict[int, list] = {}
+
+
+def _side_streams(device: torch.device, n: int) -> list:
+    """``n`` reusable streams of the default priority on ``device``."""
+    idx = torch.device(device).index
+    pool = _SIDE_STREAMS.setdefault(idx, [])
+    while len(pool) < n:
+        pool.append(torch.cuda.Stream(device=device))
+    return pool[:n]
+
+
+def _quantize_one(W, U, perm, dead, bits, group_size, blocksize, want_dequant) -> LayerResult:
+    N, K = W.shape
+    gs = group_size if 0 < group_size < K else (K if group_size > 0 else -1)
+    scale = zero = None
+    if gs <= 0:
+        scale, zero = _ops.minmax_params(W.float(), bits, -1, 0)
+    Wp = _ops.prepare_weight(W, perm=perm, dead=dead)
+    res = _ops.quantize_sweep(Wp, U, bits, gs, blocksize, L.SWEEP_TRAILING, out_cols=perm,
+                              dequant_dtype=W.dtype if want_dequant else None, scale=scale, zero=zero,
+                              want_losses=True, want_err=False)
+    del Wp
+    ar = torch.arange(K, device=W.device, dtype=torch.int32)
+    gcol = ar // gs if gs > 0 else torch.zeros_like(ar)
+    if perm is None:
+        g_idx = gcol
+    else:
+        g_idx = torch.empty_like(ar)
+        g_idx[perm.long()] = gcol
+    return LayerResult(codes=res["codes"], qweight=_ops.pack(res["codes"], bits), scale=res["scale"],
+                       zero=res["zero"], g_idx=g_idx, dequant=res["dequant"], losses_sum=res["losses"].sum())
+
+
 def quantize_layers(weights: Dict[str, torch.Tensor], hkeys: Dict[str, str],
                     hessians: Dict[str, Tuple[torch.Tensor, int]], bits: int = 4, group_size: int = 128,
                     blocksize: int = 128, percdamp: float = 0.01, actorder: bool = False,
-                    want_dequant: bool = True, check: bool = True) -> Dict[str, LayerResult]:
+                    want_dequant: bool = True, check: bool = True, streams: int = 4) -> Dict[str, LayerResult]:
     """GPTQ (canonical) on every layer in ``weights`` (name -> (N, K) weight),
-    with Hessian ``hessians[hkeys[name]]`` = (sum x x^T, nsamples)."""
-    factors = {}
+    with Hessian ``hessians[hkeys[name]]`` = (sum x x^T, nsamples).  Results
+    are ordered after the caller's current stream on return."""
+    keys = list(dict.fromkeys(hkeys[n] for n in weights))
+    dev = next(iter(weights.values())).device
+    main = torch.cuda.current_stream(dev)
+    # longest chains (largest K, then most rows) first, so they start first
+    cost = {k: (hessians[k][0].shape[0], sum(weights[n].shape[0] for n in weights if hkeys[n] == k)) for k in keys}
+    keys.sort(key=lambda k: cost[k], reverse=True)
+    pool = _side_streams(dev, max(1, min(streams, len(keys))))
+    for st in pool:
+        st.wait_stream(main)
     infos = []
-    for key in dict.fromkeys(hkeys[n] for n in weights):
-        H, ns = hessians[key]
-        factors[key] = factorize(H, ns, percdamp, actorder)
-        infos.append(factors[key][3])
     out = {}
-    for name, W in weights.items():
-        U, perm, dead, _ = factors[hkeys[name]]
-        N, K = W.shape
-        gs = group_size if 0 < group_size < K else (K if group_size > 0 else -1)
-        scale = zero = None
-        if gs <= 0:
-            scale, zero = _ops.minmax_params(W.float(), bits, -1, 0)
-        Wp = _ops.prepare_weight(W, perm=perm, dead=dead)
-        res = _ops.quantize_sweep(Wp, U, bits, gs, blocksize, L.SWEEP_TRAILING, out_cols=perm,
-                                  dequant_dtype=W.dtype if want_dequant else None, scale=scale, zero=zero,
-                                  want_losses=True, want_err=False)
-        del Wp
-        ar = torch.arange(K, device=W.device, dtype=torch.int32)
-        gcol = ar // gs if gs > 0 else torch.zeros_like(ar)
-        if perm is None:
-            g_idx = gcol
-        else:
-            g_idx = torch.empty_like(ar)
-            g_idx[perm.long()] = gcol
-        out[name] = LayerResult(codes=res["codes"], qweight=_ops.pack(res["codes"], bits), scale=res["scale"],
-                                zero=res["zero"], g_idx=g_idx, dequant=res["dequant"],
-                                losses_sum=res["losses"].sum())
+    for i, key in enumerate(keys):
+        st = pool[i % len(pool)]
+        with torch.cuda.stream(st):
+            H, ns = hessians[key]
+            U, perm, dead, info = factorize(H, ns, percdamp, actorder)
+            infos.append(info)
+            for name, W in weights.items():
+                if hkeys[name] == key:
+                    out[name] = _quantize_one(W, U, perm, dead, bits, group_size, blocksize, want_dequant)
+    for st in pool:
+        main.wait_stream(st)
+    out = {name: out[name] for name in weights}
     if check:
         bad = torch.stack([i.reshape(()) for i in infos]).cpu()
         if bool((bad != 0).any()):
