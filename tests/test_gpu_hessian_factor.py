@@ -30,6 +30,23 @@ def test_hessian_matches_fp64(hip, dtype, n, K):
     assert np.array_equal(Hn, Hn.T), "H must be exactly symmetric"
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_hessian_many_splits(hip, dtype):
+    """Enough tokens for many token splits per tile (each split a partial
+    tile, reduced in fixed order); ragged last stage."""
+    from distributed_gptq_amd import _ops
+    n, K = 65536 + 40, 1024
+    g = torch.Generator(device="cpu").manual_seed(5)
+    X = torch.randn(n, K, generator=g)
+    X[:, 7] *= 30
+    Xd = X.to(dtype).cuda()
+    H = torch.zeros(K, K, device="cuda")
+    _ops.hessian_accumulate(H, Xd)
+    Xn = Xd.double().cpu().numpy()
+    assert _rel(H.cpu().numpy(), Xn.T @ Xn) < 1e-5
+    assert torch.equal(H, H.T)
+
+
 def test_hessian_accumulates_and_nonaligned_rows(hip):
     from distributed_gptq_amd import _ops
     K = 520
