@@ -82,154 +82,169 @@ __global__ void fill_zero(float* __restrict__ p, int64_t n) {
     p[i] = 0.0f;
 }
 
-// One workgroup of 256 threads: Cholesky of the m x m (m <= 128) diagonal
-// block of A at (n0, n0) and the inverse of its factor.  Thread (ti, tk) of a
-// 16 x 16 grid keeps rows 8*ti..8*ti+7, columns 8*tk..8*tk+7 of the block in
-// registers; each right-looking step publishes only the next pivot column
-// (Cholesky) or the next scaled row (inverse) through a double-buffered LDS
-// vector, so a step costs one barrier, 16 LDS reads and 64 FMAs per thread.
-// Writes L (zeros above) into A and X = L^-1 (zeros above) into X.  A
-// non-positive pivot records info = 1 + (column in A order) once.
-constexpr int kLP = kNB + 1;  // LDS pitch of L
-constexpr size_t kLeafLds = sizeof(float) * (2 * kNB + kNB * kLP + 2 * kNB);
+// One workgroup of 4 waves: Cholesky of the m x m (m <= 128) diagonal block
+// of A at (n0, n0) and the inverse of its factor, blocked by 32:
+//   for each diagonal block k:  one wave factors D_kk = L_kk L_kk^T and
+//     inverts L_kk (X_kk) in registers, broadcasting with v_readlane (no
+//     barriers); then L_ik = A_ik X_kk^T (panel) and A_ij -= L_ik L_jk^T
+//     (trailing) as 32x32x32 v_mfma_f32_32x32x2f32 products, one per wave;
+//   then X_ij (i > j) = -X_ii sum_{k=j}^{i-1} L_ik X_kj by block distance.
+// The tile is padded to 128 with the identity.  Writes L (zeros above) into
+// A and X = L^-1 (zeros above) into X; a non-positive pivot records
+// info = 1 + (column in A order) once.
+constexpr int kLP = kNB + 1;  // LDS pitch (odd: conflict-free column reads)
+constexpr int kLB = 32;       // diagonal block
+constexpr size_t kLeafLds = sizeof(float) * (2 * kNB * kLP + 4 * kLB * (kLB + 1));
+
+__device__ __forceinline__ float rdl(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+// acc += P (32 x 32 at pa, rows r, k) x Q' where Q' = Q^T (Q[c][k] at pb) when
+// bT, else Q (Q[k][c] at pb); one wave, 16 steps of v_mfma_f32_32x32x2f32
+// (lane l: operand row/column l % 32, k = 2 s + l / 32)
+__device__ __forceinline__ f32x16 mm32(const float* pa, int lda, const float* pb, int ldb, bool bT, f32x16 acc,
+                                      int lane) {
+  const int i = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int st = 0; st < 16; ++st) {
+    const int k = 2 * st + h;
+    const float x = pa[i * lda + k];
+    const float y = bT ? pb[i * ldb + k] : pb[k * ldb + i];
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x, y, acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+// 32x32 accumulator layout: lane l, register v -> row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32
+__device__ __forceinline__ void put32(float* pc, int ldc, const f32x16& acc, float scale, int lane) {
+#pragma unroll
+  for (int v = 0; v < 16; ++v) pc[(8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) * ldc + (lane & 31)] = scale * acc[v];
+}
+
+// One wave: D (32 x 32 at sD) = L L^T in registers (lane r holds row r), L
+// written back over D (zeros above) and X = L^-1 written to sXd (lane c
+// computes column c by forward substitution).
+__device__ __forceinline__ void diag32(float* sD, float* sXd, int lane, int col0, int lim, int& first_bad) {
+  const int r = lane & 31;
+  float a[kLB];
+#pragma unroll
+  for (int c = 0; c < kLB; ++c) a[c] = sD[r * kLP + c];
+  float mydiag = 1.0f;
+#pragma unroll
+  for (int j = 0; j < kLB; ++j) {
+    const float piv = rdl(a[j], j);
+    if (!(piv > 0.0f) && first_bad < 0 && col0 + j < lim) first_bad = col0 + j;
+    const float d = sqrtf(piv);
+    const float inv = 1.0f / d;
+    const float l = (r > j) ? a[j] * inv : (r == j ? d : 0.0f);
+    a[j] = l;
+    if (r == j) mydiag = d;
+#pragma unroll
+    for (int c = j + 1; c < kLB; ++c) a[c] = fmaf(-l, rdl(l, c), a[c]);
+    __builtin_amdgcn_sched_barrier(0);  // keep the broadcasts of one step together (scalar registers)
+  }
+  const float myinv = 1.0f / mydiag;
+  float x[kLB];
+#pragma unroll
+  for (int rr = 0; rr < kLB; ++rr) {
+    float t = (r == rr) ? 1.0f : 0.0f;
+#pragma unroll
+    for (int k = 0; k < rr; ++k) t = fmaf(-rdl(a[k], rr), x[k], t);
+    x[rr] = t * rdl(myinv, rr);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (lane < kLB) {
+#pragma unroll
+    for (int c = 0; c < kLB; ++c) sD[r * kLP + c] = (c <= r) ? a[c] : 0.0f;
+#pragma unroll
+    for (int rr = 0; rr < kLB; ++rr) sXd[rr * kLP + r] = x[rr];
+  }
+}
 
 __global__ __launch_bounds__(256) void chol_inv_leaf(float* __restrict__ A, float* __restrict__ X, int64_t ld,
                                                      int64_t n0, int m, int32_t* __restrict__ info) {
   extern __shared__ float lds[];
-  float* col = lds;                  // [2][kNB]
-  float* Ls = lds + 2 * kNB;         // [kNB][kLP]
-  float* xrow = Ls + kNB * kLP;      // [2][kNB]
+  float* sA = lds;                      // [128][kLP]: A, then L
+  float* sX = lds + kNB * kLP;          // [128][kLP]: X
+  float* sS = sX + kNB * kLP;           // [wave][32][33]: partial sums of the inverse
   const int tid = threadIdx.x;
-  const int ti = tid >> 4, tk = tid & 15;
-  const int R0 = 8 * ti, C0 = 8 * tk;
-  float a[8][8];
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  constexpr int NB = kNB / kLB;
+
+  // load the lower triangle (identity padding beyond m), eight loads in flight per thread
+  for (int e0 = tid; e0 < kNB * kNB; e0 += 256 * 8) {
+    float v[8];
 #pragma unroll
-  for (int u = 0; u < 8; ++u)
-#pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      const int r = R0 + u, c = C0 + v;
-      a[u][v] = (r < m && c <= r) ? A[(n0 + r) * ld + n0 + c] : 0.0f;
+    for (int u = 0; u < 8; ++u) {
+      const int e = e0 + u * 256;
+      const int rr = e >> 7, cc = e & (kNB - 1);
+      v[u] = (rr < m && cc < m && cc <= rr) ? A[(n0 + rr) * ld + n0 + cc] : (rr == cc ? 1.0f : 0.0f);
     }
-  if (tk == 0) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) col[R0 + u] = a[u][0];
+    for (int u = 0; u < 8; ++u) {
+      const int e = e0 + u * 256;
+      sA[(e >> 7) * kLP + (e & (kNB - 1))] = v[u];
+      sX[(e >> 7) * kLP + (e & (kNB - 1))] = 0.0f;
+    }
   }
   __syncthreads();
+
   int first_bad = -1;
-  for (int j = 0; j < m; ++j) {
-    const float* cj = col + (j & 1) * kNB;
-    const float p = cj[j];
-    if (!(p > 0.0f) && first_bad < 0) first_bad = j;
-    const float d = sqrtf(p);
-    const float inv = 1.0f / d;
-    if (R0 + 7 >= j) {
-      // unconditional vector reads, masked afterwards (a guarded read would
-      // become a branch with its own LDS round trip)
-      float cr[8], cc[8];
-      *reinterpret_cast<f32x4*>(cr) = *reinterpret_cast<const f32x4*>(cj + R0);
-      *reinterpret_cast<f32x4*>(cr + 4) = *reinterpret_cast<const f32x4*>(cj + R0 + 4);
-      *reinterpret_cast<f32x4*>(cc) = *reinterpret_cast<const f32x4*>(cj + C0);
-      *reinterpret_cast<f32x4*>(cc + 4) = *reinterpret_cast<const f32x4*>(cj + C0 + 4);
-      float lr[8], lc[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) lr[u] = (R0 + u > j) ? cr[u] * inv : 0.0f;
-#pragma unroll
-      for (int v = 0; v < 8; ++v) lc[v] = (C0 + v > j) ? cc[v] * inv : 0.0f;
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-#pragma unroll
-        for (int v = 0; v < 8; ++v) a[u][v] -= lr[u] * lc[v];
-      if (C0 <= j && j < C0 + 8) {
-        // column j of L: l = a / d below the diagonal, d on it
-#pragma unroll
-        for (int v = 0; v < 8; ++v)
-          if (C0 + v == j) {
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-              const int r = R0 + u;
-              if (r > j) a[u][v] = lr[u];
-              else if (r == j) a[u][v] = d;
-            }
-          }
+  auto blk = [&](float* base, int bi, int bj) { return base + bi * kLB * kLP + bj * kLB; };
+  for (int kb = 0; kb < NB; ++kb) {
+    if (wave == 0) diag32(blk(sA, kb, kb), blk(sX, kb, kb), lane, kb * kLB, m, first_bad);
+    __syncthreads();
+    // panel: L_ik = A_ik X_kk^T, one wave per block row
+    {
+      const int ib = kb + 1 + wave;
+      if (ib < NB) {
+        f32x16 acc = {};
+        acc = mm32(blk(sA, ib, kb), kLP, blk(sX, kb, kb), kLP, true, acc, lane);
+        put32(blk(sA, ib, kb), kLP, acc, 1.0f, lane);
       }
-      const int jn = j + 1;
-      if (jn < m && C0 <= jn && jn < C0 + 8) {
-        float* cn = col + (jn & 1) * kNB;
+    }
+    __syncthreads();
+    // trailing: A_ij -= L_ik L_jk^T for kb < j <= i
+    {
+      int t = 0;
+      for (int ib = kb + 1; ib < NB; ++ib)
+        for (int jb = kb + 1; jb <= ib; ++jb, ++t) {
+          if ((t & 3) != wave) continue;
+          f32x16 acc = {};
+          acc = mm32(blk(sA, ib, kb), kLP, blk(sA, jb, kb), kLP, true, acc, lane);
+          float* pc = blk(sA, ib, jb);
 #pragma unroll
-        for (int v = 0; v < 8; ++v)
-          if (C0 + v == jn) {
-#pragma unroll
-            for (int u = 0; u < 8; ++u) cn[R0 + u] = a[u][v];
+          for (int v = 0; v < 16; ++v) {
+            float& c = pc[(8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) * kLP + (lane & 31)];
+            c -= acc[v];
           }
-      }
+        }
+    }
+    __syncthreads();
+  }
+  // X_ij = -X_ii S, S = sum_{k=j}^{i-1} L_ik X_kj, by block distance
+  for (int d = 1; d < NB; ++d) {
+    const int jb = wave, ib = wave + d;
+    if (ib < NB) {
+      f32x16 acc = {};
+      for (int k = jb; k < ib; ++k) acc = mm32(blk(sA, ib, k), kLP, blk(sX, k, jb), kLP, false, acc, lane);
+      float* ps = sS + wave * kLB * (kLB + 1);
+      put32(ps, kLB + 1, acc, 1.0f, lane);
+      f32x16 acc2 = {};
+      acc2 = mm32(blk(sX, ib, ib), kLP, ps, kLB + 1, false, acc2, lane);
+      put32(blk(sX, ib, jb), kLP, acc2, -1.0f, lane);
     }
     __syncthreads();
   }
   if (first_bad >= 0 && tid == 0) atomicCAS(info, 0, static_cast<int32_t>(n0 + first_bad + 1));
-#pragma unroll
-  for (int u = 0; u < 8; ++u)
-#pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      const int r = R0 + u, c = C0 + v;
-      const float val = (c <= r) ? a[u][v] : 0.0f;
-      Ls[r * kLP + c] = val;
-      if (r < m && c < m) A[(n0 + r) * ld + n0 + c] = val;
-    }
-  __syncthreads();
-  // X = L^-1, right-looking on rows: row j is scaled by 1/L[j][j] when it is
-  // published, then subtracted from the rows below with weights L[r][j]
-  float x[8][8];
-#pragma unroll
-  for (int u = 0; u < 8; ++u)
-#pragma unroll
-    for (int v = 0; v < 8; ++v) x[u][v] = (R0 + u == C0 + v && R0 + u < m) ? 1.0f : 0.0f;
-  if (ti == 0) {
-    const float s0 = 1.0f / Ls[0];
-#pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      x[0][v] *= s0;
-      xrow[C0 + v] = x[0][v];
-    }
+  // write back L and X (lower, zeros above) for the m x m block
+  for (int e = tid; e < m * m; e += 256) {
+    const int rr = e / m, cc = e - (e / m) * m;
+    A[(n0 + rr) * ld + n0 + cc] = (cc <= rr) ? sA[rr * kLP + cc] : 0.0f;
+    X[(n0 + rr) * ld + n0 + cc] = (cc <= rr) ? sX[rr * kLP + cc] : 0.0f;
   }
-  __syncthreads();
-  for (int j = 0; j < m; ++j) {
-    const float* xj = xrow + (j & 1) * kNB;
-    if (R0 + 7 > j) {
-      float lt[8], lr[8], xc[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) lt[u] = Ls[(R0 + u) * kLP + j];
-      *reinterpret_cast<f32x4*>(xc) = *reinterpret_cast<const f32x4*>(xj + C0);
-      *reinterpret_cast<f32x4*>(xc + 4) = *reinterpret_cast<const f32x4*>(xj + C0 + 4);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) lr[u] = (R0 + u > j) ? lt[u] : 0.0f;
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-#pragma unroll
-        for (int v = 0; v < 8; ++v) x[u][v] -= lr[u] * xc[v];
-      const int jn = j + 1;
-      if (jn < m && R0 <= jn && jn < R0 + 8) {
-        const float sn = 1.0f / Ls[jn * kLP + jn];
-        float* xn = xrow + (jn & 1) * kNB;
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-          if (R0 + u == jn) {
-#pragma unroll
-            for (int v = 0; v < 8; ++v) {
-              x[u][v] *= sn;
-              xn[C0 + v] = x[u][v];
-            }
-          }
-      }
-    }
-    __syncthreads();
-  }
-#pragma unroll
-  for (int u = 0; u < 8; ++u)
-#pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      const int r = R0 + u, c = C0 + v;
-      if (r < m && c < m) X[(n0 + r) * ld + n0 + c] = (c <= r) ? x[u][v] : 0.0f;
-    }
 }
 
 // in-place U = J X J over the full K x K matrix (swap (i,j) <-> (K-1-i, K-1-j))

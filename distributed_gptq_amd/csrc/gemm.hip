@@ -143,21 +143,37 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(int64_t M, int64_t N
     }
   }
 
+  // Epilogue, one 32 x 32 block at a time: its 16 reads of C are issued
+  // before its stores (interleaved, each store would wait for the read
+  // before it -- the compiler cannot tell the addresses apart -- one memory
+  // round trip per element instead of one per block).
   const bool lower = (flags & GEMM_C_LOWER) != 0;
+  const int64_t rbase = i0 + wm + 4 * (lane >> 5);
+  const int64_t cbase = j0 + wn + (lane & 31);
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 2; ++j) {
+      const int64_t col = cbase + j * 32;
+      float* cp = C + (rbase + i * 32) * ldc + col;
+      float cv[16];
+      if (beta != 0.0f) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t row = i0 + wm + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        const int64_t col = j0 + wn + j * 32 + (lane & 31);
-        if (row < M && col < N && (!lower || row >= col)) {
-          float r = alpha * acc[i][j][v];
-          if (beta != 0.0f) r += beta * C[row * ldc + col];
-          C[row * ldc + col] = r;
+        for (int v = 0; v < 16; ++v) {
+          const int64_t row = rbase + i * 32 + 8 * (v >> 2) + (v & 3);
+          cv[v] = (row < M && col < N) ? cp[(8 * (v >> 2) + (v & 3)) * ldc] : 0.0f;
         }
       }
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t row = rbase + i * 32 + 8 * (v >> 2) + (v & 3);
+        if (row < M && col < N && (!lower || row >= col)) {
+          float r = alpha * acc[i][j][v];
+          if (beta != 0.0f) r += beta * cv[v];
+          cp[(8 * (v >> 2) + (v & 3)) * ldc] = r;
+        }
+      }
+    }
 }
 
 }  // namespace

@@ -230,11 +230,23 @@ constexpr int kRowWaves = 2;  // waves (64 rows each) per workgroup
 constexpr int kTt = 132;      // row pitch of Tt in floats (16-byte aligned)
 constexpr int kMaxG = 6;      // groups a 128-column sub-block can touch when g >= 32
 
+// a / b from a correctly rounded reciprocal rb of b: one FMA residual step
+// (Markstein), so the quotient is the correctly rounded one except in rare
+// near-midpoint cases, at three dependent operations instead of an IEEE
+// division sequence on the column recurrence
+__device__ __forceinline__ float div_rcp(float a, float b, float rb) {
+  const float q0 = a * rb;
+  const float r = fmaf(-q0, b, a);
+  return fmaf(r, rb, q0);
+}
+
+template <bool REF>
 __global__ __launch_bounds__(64 * kRowWaves) void sweep_rows(SubArgs a) {
   extern __shared__ float smem[];
   float* Tt = smem;                                   // 128 x kTt
   float* ws_all = smem + 128 * kTt;                   // [wave][128][64]
   float* prm_all = ws_all + kRowWaves * 128 * 64;     // [wave][kMaxG][2][64]
+  float* invd = prm_all + kRowWaves * kMaxG * 2 * 64;  // [128] 1 / T[j][j]
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -242,9 +254,48 @@ __global__ __launch_bounds__(64 * kRowWaves) void sweep_rows(SubArgs a) {
   float* ws = ws_all + wave * 128 * 64;
   float* prm = prm_all + wave * kMaxG * 2 * 64;
 
-  for (int e = tid; e < n * n; e += 64 * kRowWaves) {
-    const int r = e / n, c = e - (e / n) * n;
-    Tt[c * kTt + r] = a.T[(a.j1 + r) * a.ldt + a.j1 + c];
+  // Stage the T block transposed (Tt[c][r]) and this lane's row of W (ws),
+  // with eight loads per thread in flight before any is stored: a load-then-
+  // store loop would pay one memory round trip per element.
+  constexpr int kThr = 64 * kRowWaves;
+  constexpr int kBatch = 8;
+  const float* tsrc = a.T + a.j1 * a.ldt + a.j1;
+  if ((n & 3) == 0 && (a.ldt & 3) == 0 && (reinterpret_cast<uintptr_t>(tsrc) & 15) == 0) {
+    // vector e covers columns 4 (e / n) .. +3 of row e % n (consecutive
+    // threads, consecutive rows: conflict-free transposed stores)
+    const int tot = n * (n >> 2);
+    for (int e0 = tid; e0 < tot; e0 += kThr * kBatch) {
+      f32x4 v[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int e = e0 + u * kThr;
+        if (e < tot) v[u] = *reinterpret_cast<const f32x4*>(tsrc + (e % n) * a.ldt + 4 * (e / n));
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int e = e0 + u * kThr;
+        if (e < tot) {
+          const int r = e % n, c = 4 * (e / n);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) Tt[(c + q) * kTt + r] = v[u][q];
+        }
+      }
+    }
+  } else {
+    const int tot = n * n;
+    for (int e0 = tid; e0 < tot; e0 += kThr * kBatch) {
+      float v[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int e = e0 + u * kThr;
+        if (e < tot) v[u] = tsrc[(e % n) * a.ldt + e / n];
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int e = e0 + u * kThr;
+        if (e < tot) Tt[(e / n) * kTt + e % n] = v[u];
+      }
+    }
   }
   const int64_t row = static_cast<int64_t>(blockIdx.x) * (64 * kRowWaves) + wave * 64 + lane;
   const bool valid = row < a.rows;
@@ -253,12 +304,14 @@ __global__ __launch_bounds__(64 * kRowWaves) void sweep_rows(SubArgs a) {
     const float* src = a.W + rrow * a.cols + a.j1;
     int c = 0;
     if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {
-      for (; c + 4 <= n; c += 4) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(src + c);
-        ws[c * 64 + lane] = v[0];
-        ws[(c + 1) * 64 + lane] = v[1];
-        ws[(c + 2) * 64 + lane] = v[2];
-        ws[(c + 3) * 64 + lane] = v[3];
+      for (; c + 4 * kBatch <= n; c += 4 * kBatch) {
+        f32x4 v[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) v[u] = *reinterpret_cast<const f32x4*>(src + c + 4 * u);
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) ws[(c + 4 * u + q) * 64 + lane] = v[u][q];
       }
     }
     for (; c < n; ++c) ws[c * 64 + lane] = src[c];
@@ -267,6 +320,8 @@ __global__ __launch_bounds__(64 * kRowWaves) void sweep_rows(SubArgs a) {
     prm[(g * 2) * 64 + lane] = a.scale[rrow * a.ngroups + a.g_lo + g];
     prm[(g * 2 + 1) * 64 + lane] = a.zero[rrow * a.ngroups + a.g_lo + g];
   }
+  __syncthreads();
+  for (int j = tid; j < n; j += kThr) invd[j] = 1.0f / Tt[j * kTt + j];
   __syncthreads();
 
   const float fmaxq = static_cast<float>(a.maxq);
@@ -283,6 +338,7 @@ __global__ __launch_bounds__(64 * kRowWaves) void sweep_rows(SubArgs a) {
     const float s0 = prm[(g0 * 2) * 64 + lane], z0 = prm[(g0 * 2 + 1) * 64 + lane];
     const int g1 = (g0 + 1 < a.G) ? g0 + 1 : g0;
     const float s1 = prm[(g1 * 2) * 64 + lane], z1 = prm[(g1 * 2 + 1) * 64 + lane];
+    const float is0 = 1.0f / s0, is1 = 1.0f / s1;
     float ep[kPW], qp[kPW], dp[kPW], lp[kPW];
 #pragma unroll
     for (int i = 0; i < kPW; ++i) {
@@ -303,20 +359,22 @@ __global__ __launch_bounds__(64 * kRowWaves) void sweep_rows(SubArgs a) {
         w -= (acc[0] + acc[1]) + (acc[2] + acc[3]);
         const bool second = i >= brk;
         const float s = second ? s1 : s0;
+        const float is = second ? is1 : is0;
         const float z = second ? z1 : z0;
+        const float t = div_rcp(w, s, is);
         float q;
-        if (a.ref)
-          q = fminf(fmaxf(rintf(w / s + z), 0.0f), fmaxq);
+        if constexpr (REF)
+          q = fminf(fmaxf(rintf(t + z), 0.0f), fmaxq);
         else
-          q = fminf(fmaxf(rintf(w / s) + z, 0.0f), fmaxq);
+          q = fminf(fmaxf(rintf(t) + z, 0.0f), fmaxq);
         const float dq = s * (q - z);
         const float d = Tt[j * kTt + j];
         const float diff = w - dq;
-        const float e = diff / d;
+        const float e = div_rcp(diff, d, invd[j]);
         ep[i] = e;
         qp[i] = q;
         dp[i] = dq;
-        lp[i] = diff * diff / (d * d) * 0.5f;
+        lp[i] = 0.5f * e * e;
         esq += e * e;
       }
     }
@@ -435,8 +493,11 @@ __global__ void prepare_weight_k(const void* __restrict__ w, int dtype, int64_t 
 
 int launch_rows(hipStream_t st, const SubArgs& a) {
   const unsigned blocks = static_cast<unsigned>(cdiv(a.rows, 64LL * kRowWaves));
-  const size_t lds = sizeof(float) * (128 * kTt + kRowWaves * 128 * 64 + kRowWaves * kMaxG * 2 * 64);
-  hipLaunchKernelGGL(sweep_rows, dim3(blocks), dim3(64 * kRowWaves), lds, st, a);
+  const size_t lds = sizeof(float) * (128 * kTt + kRowWaves * 128 * 64 + kRowWaves * kMaxG * 2 * 64 + 128);
+  if (a.ref)
+    hipLaunchKernelGGL(sweep_rows<true>, dim3(blocks), dim3(64 * kRowWaves), lds, st, a);
+  else
+    hipLaunchKernelGGL(sweep_rows<false>, dim3(blocks), dim3(64 * kRowWaves), lds, st, a);
   return check_launch("sweep_rows");
 }
 

@@ -19,7 +19,7 @@ of the same device) and overlap on the GPU.
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Dict, Optional, Tuple
+from typing import Dict, Optional, Sequence, Tuple, Union
 
 import torch
 
@@ -54,7 +54,7 @@ def factorize(H: torch.Tensor, nsamples: int, percdamp: float, actorder: bool):
 _SIDE_STREAMS: Dict[int, list] = {}
 
 
-def _side_streams(device: torch.device, n: int) -> list:
+def side_streams(device: torch.device, n: int) -> list:
     """``n`` reusable streams of the default priority on ``device``."""
     idx = torch.device(device).index
     pool = _SIDE_STREAMS.setdefault(idx, [])
@@ -85,20 +85,45 @@ def _quantize_one(W, U, perm, dead, bits, group_size, blocksize, want_dequant) -
                        zero=res["zero"], g_idx=g_idx, dequant=res["dequant"], losses_sum=res["losses"].sum())
 
 
-def quantize_layers(weights: Dict[str, torch.Tensor], hkeys: Dict[str, str],
-                    hessians: Dict[str, Tuple[torch.Tensor, int]], bits: int = 4, group_size: int = 128,
-                    blocksize: int = 128, percdamp: float = 0.01, actorder: bool = False,
-                    want_dequant: bool = True, check: bool = True, streams: int = 4) -> Dict[str, LayerResult]:
-    """GPTQ (canonical) on every layer in ``weights`` (name -> (N, K) weight),
-    with Hessian ``hessians[hkeys[name]]`` = (sum x x^T, nsamples).  Results
-    are ordered after the caller's current stream on return."""
+class PendingLayers:
+    """Layers being quantized on side streams; ``wait()`` orders the caller's
+    current stream after them, checks positive-definiteness (one host sync)
+    and returns the results."""
+
+    def __init__(self, out, infos, streams, order, check):
+        self._out, self._infos, self._streams, self._order, self._check = out, infos, streams, order, check
+
+    def wait(self) -> Dict[str, LayerResult]:
+        main = torch.cuda.current_stream(self._streams[0].device)
+        for st in self._streams:
+            main.wait_stream(st)
+        if self._check:
+            bad = torch.stack([i.reshape(()) for i in self._infos]).cpu()
+            if bool((bad != 0).any()):
+                raise torch.linalg.LinAlgError("a damped Hessian is not positive-definite")
+        return {name: self._out[name] for name in self._order}
+
+
+def quantize_layers_async(weights: Dict[str, torch.Tensor], hkeys: Dict[str, str],
+                          hessians: Dict[str, Tuple[torch.Tensor, int]], bits: int = 4, group_size: int = 128,
+                          blocksize: int = 128, percdamp: float = 0.01, actorder: bool = False,
+                          want_dequant: bool = True, check: bool = True,
+                          streams: Union[int, Sequence[torch.cuda.Stream]] = 4) -> PendingLayers:
+    """Starts GPTQ (canonical) on every layer in ``weights`` (name -> (N, K)
+    weight) with Hessian ``hessians[hkeys[name]]`` = (sum x x^T, nsamples):
+    each Hessian's chain on one of ``streams`` (a count taken from a reusable
+    pool, or explicit streams), after the work already enqueued on the
+    caller's current stream.  Returns without waiting."""
     keys = list(dict.fromkeys(hkeys[n] for n in weights))
     dev = next(iter(weights.values())).device
     main = torch.cuda.current_stream(dev)
     # longest chains (largest K, then most rows) first, so they start first
     cost = {k: (hessians[k][0].shape[0], sum(weights[n].shape[0] for n in weights if hkeys[n] == k)) for k in keys}
     keys.sort(key=lambda k: cost[k], reverse=True)
-    pool = _side_streams(dev, max(1, min(streams, len(keys))))
+    if isinstance(streams, int):
+        pool = side_streams(dev, max(1, min(streams, len(keys))))
+    else:
+        pool = list(streams)
     for st in pool:
         st.wait_stream(main)
     infos = []
@@ -112,11 +137,16 @@ def quantize_layers(weights: Dict[str, torch.Tensor], hkeys: Dict[str, str],
             for name, W in weights.items():
                 if hkeys[name] == key:
                     out[name] = _quantize_one(W, U, perm, dead, bits, group_size, blocksize, want_dequant)
-    for st in pool:
-        main.wait_stream(st)
-    out = {name: out[name] for name in weights}
-    if check:
-        bad = torch.stack([i.reshape(()) for i in infos]).cpu()
-        if bool((bad != 0).any()):
-            raise torch.linalg.LinAlgError("a damped Hessian is not positive-definite")
-    return out
+    return PendingLayers(out, infos, pool, list(weights), check)
+
+
+def quantize_layers(weights: Dict[str, torch.Tensor], hkeys: Dict[str, str],
+                    hessians: Dict[str, Tuple[torch.Tensor, int]], bits: int = 4, group_size: int = 128,
+                    blocksize: int = 128, percdamp: float = 0.01, actorder: bool = False,
+                    want_dequant: bool = True, check: bool = True,
+                    streams: Union[int, Sequence[torch.cuda.Stream]] = 4) -> Dict[str, LayerResult]:
+    """GPTQ (canonical) on every layer in ``weights`` (name -> (N, K) weight),
+    with Hessian ``hessians[hkeys[name]]`` = (sum x x^T, nsamples).  Results
+    are ordered after the caller's current stream on return."""
+    return quantize_layers_async(weights, hkeys, hessians, bits, group_size, blocksize, percdamp, actorder,
+                                 want_dequant, check, streams).wait()
