@@ -1,20 +1,19 @@
 // fp32 GEMM on v_mfma_f32_32x32x2_f32 (gfx950).
 //
-// 128 x 128 output tile per workgroup of 4 waves (2 x 2, 64 x 64 each =
-// 2 x 2 MFMA 32x32 blocks), 16-deep k stages staged in LDS as [row][k]
-// (pitch 18 floats: the two k-rows a 32x32x2 fragment reads land in
+// TM x TN output tile per workgroup of 4 waves (2 x 2, each TM/2 x TN/2 =
+// FM x FN MFMA 32x32 blocks), BK-deep k stages staged in LDS as [row][k]
+// (pitch BK + 2 floats: the two k-rows a 32x32x2 fragment reads land in
 // disjoint bank halves), next stage prefetched into registers while the
-// current one is multiplied.  Triangular operands skip the k-tiles that are
-// known to be zero; GEMM_C_LOWER skips tiles strictly above the diagonal.
+// current one is multiplied.  Large products use 128 x 128 tiles, 16 deep;
+// products that would give fewer than 128 such tiles use 64 x 64 tiles, 32
+// deep (four times the workgroups, half the stages).  Triangular operands
+// skip the k-tiles that are known to be zero; GEMM_C_LOWER skips tiles
+// strictly above the diagonal.
 #include "gemm.hpp"
 
 namespace gptq {
 namespace {
 
-constexpr int kTM = 128;
-constexpr int kTN = 128;
-constexpr int kBK = 16;
-constexpr int kPitch = kBK + 2;
 constexpr int kThreads = 256;
 
 struct Operand {
@@ -24,19 +23,20 @@ struct Operand {
   int64_t rows; // extent along r
 };
 
-// Loads the stage (r0..r0+127, k0..k0+15) of an operand viewed as [r][k]
-// into registers: 512 float4 per operand, 2 per thread.
-template <bool kVec>
+// Loads the stage (r0..r0+TR-1, k0..k0+BK-1) of an operand viewed as [r][k]
+// into registers: TR * BK / 4 float4, NQ per thread.
+template <int TR, int BK, bool kVec>
 __device__ __forceinline__ void load_op(const Operand& o, int64_t r0, int64_t k0, int64_t Kd, int tid,
-                                        f32x4 (&pre)[2]) {
+                                        f32x4 (&pre)[TR * BK / 4 / kThreads]) {
+  constexpr int NQ = TR * BK / 4 / kThreads;
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
+  for (int q = 0; q < NQ; ++q) {
     const int idx = q * kThreads + tid;
     f32x4 v = {0.f, 0.f, 0.f, 0.f};
     if (!o.trans) {
-      // contiguous along k: 4 lanes per row
-      const int64_t r = r0 + (idx >> 2);
-      const int64_t k = k0 + (idx & 3) * 4;
+      // contiguous along k: BK / 4 lanes per row
+      const int64_t r = r0 + idx / (BK / 4);
+      const int64_t k = k0 + (idx % (BK / 4)) * 4;
       if (r < o.rows) {
         const float* src = o.p + r * o.ld + k;
         if (kVec && k + 3 < Kd) {
@@ -47,9 +47,9 @@ __device__ __forceinline__ void load_op(const Operand& o, int64_t r0, int64_t k0
         }
       }
     } else {
-      // contiguous along r: 32 lanes per k-row
-      const int64_t k = k0 + (idx >> 5);
-      const int64_t r = r0 + (idx & 31) * 4;
+      // contiguous along r: TR / 4 lanes per k-row
+      const int64_t k = k0 + idx / (TR / 4);
+      const int64_t r = r0 + (idx % (TR / 4)) * 4;
       if (k < Kd) {
         const float* src = o.p + k * o.ld + r;
         if (kVec && r + 3 < o.rows) {
@@ -64,82 +64,88 @@ __device__ __forceinline__ void load_op(const Operand& o, int64_t r0, int64_t k0
   }
 }
 
-__device__ __forceinline__ void store_op(bool trans, float* s, int tid, const f32x4 (&pre)[2]) {
+template <int TR, int BK>
+__device__ __forceinline__ void store_op(bool trans, float* s, int tid, const f32x4 (&pre)[TR * BK / 4 / kThreads]) {
+  constexpr int NQ = TR * BK / 4 / kThreads;
+  constexpr int P = BK + 2;
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
+  for (int q = 0; q < NQ; ++q) {
     const int idx = q * kThreads + tid;
     if (!trans) {
-      const int r = idx >> 2, k = (idx & 3) * 4;
-      float2* d = reinterpret_cast<float2*>(s + r * kPitch + k);
+      const int r = idx / (BK / 4), k = (idx % (BK / 4)) * 4;
+      float2* d = reinterpret_cast<float2*>(s + r * P + k);
       d[0] = make_float2(pre[q][0], pre[q][1]);
       d[1] = make_float2(pre[q][2], pre[q][3]);
     } else {
-      const int k = idx >> 5, r = (idx & 31) * 4;
+      const int k = idx / (TR / 4), r = (idx % (TR / 4)) * 4;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) s[(r + e) * kPitch + k] = pre[q][e];
+      for (int e = 0; e < 4; ++e) s[(r + e) * P + k] = pre[q][e];
     }
   }
 }
 
-template <bool kVec>
+template <int TM, int TN, int BK, bool kVec>
 __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(int64_t M, int64_t N, int64_t Kd, float alpha,
                                                            Operand a, Operand b, float beta, float* __restrict__ C,
                                                            int64_t ldc, int flags, int tiles_n) {
-  __shared__ float sA[kTM * kPitch];
-  __shared__ float sB[kTN * kPitch];
+  constexpr int P = BK + 2;
+  constexpr int FM = TM / 64, FN = TN / 64;  // 32x32 blocks per wave
+  constexpr int QA = TM * BK / 4 / kThreads, QB = TN * BK / 4 / kThreads;
+  __shared__ float sA[TM * P];
+  __shared__ float sB[TN * P];
   const int tm = blockIdx.x / tiles_n;
   const int tn = blockIdx.x % tiles_n;
-  const int64_t i0 = static_cast<int64_t>(tm) * kTM;
-  const int64_t j0 = static_cast<int64_t>(tn) * kTN;
-  if ((flags & GEMM_C_LOWER) && j0 > i0 + kTM - 1) return;
+  const int64_t i0 = static_cast<int64_t>(tm) * TM;
+  const int64_t j0 = static_cast<int64_t>(tn) * TN;
+  if ((flags & GEMM_C_LOWER) && j0 > i0 + TM - 1) return;
 
   int64_t kb = 0, ke = Kd;
-  if (flags & GEMM_KLIM_A_LE_I) ke = std::min<int64_t>(ke, i0 + kTM);
-  if (flags & GEMM_KLIM_B_LE_J) ke = std::min<int64_t>(ke, j0 + kTN);
+  if (flags & GEMM_KLIM_A_LE_I) ke = std::min<int64_t>(ke, i0 + TM);
+  if (flags & GEMM_KLIM_B_LE_J) ke = std::min<int64_t>(ke, j0 + TN);
   if (flags & GEMM_KLIM_A_GE_I) kb = std::max<int64_t>(kb, i0);
   if (flags & GEMM_KLIM_B_GE_J) kb = std::max<int64_t>(kb, j0);
-  kb = (kb / kBK) * kBK;
+  kb = (kb / BK) * BK;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = (wave >> 1) * 64;
-  const int wn = (wave & 1) * 64;
+  const int wm = (wave >> 1) * (TM / 2);
+  const int wn = (wave & 1) * (TN / 2);
 
-  f32x16 acc[2][2];
+  f32x16 acc[FM][FN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  f32x4 pa[2], pb[2];
+  f32x4 pa[QA], pb[QB];
   if (kb < ke) {
-    load_op<kVec>(a, i0, kb, Kd, tid, pa);
-    load_op<kVec>(b, j0, kb, Kd, tid, pb);
+    load_op<TM, BK, kVec>(a, i0, kb, Kd, tid, pa);
+    load_op<TN, BK, kVec>(b, j0, kb, Kd, tid, pb);
   }
-  for (int64_t k0 = kb; k0 < ke; k0 += kBK) {
+  for (int64_t k0 = kb; k0 < ke; k0 += BK) {
     __syncthreads();
-    store_op(a.trans, sA, tid, pa);
-    store_op(b.trans, sB, tid, pb);
+    store_op<TM, BK>(a.trans, sA, tid, pa);
+    store_op<TN, BK>(b.trans, sB, tid, pb);
     __syncthreads();
-    if (k0 + kBK < ke) {
-      load_op<kVec>(a, i0, k0 + kBK, Kd, tid, pa);
-      load_op<kVec>(b, j0, k0 + kBK, Kd, tid, pb);
+    if (k0 + BK < ke) {
+      load_op<TM, BK, kVec>(a, i0, k0 + BK, Kd, tid, pa);
+      load_op<TN, BK, kVec>(b, j0, k0 + BK, Kd, tid, pb);
     }
 #pragma unroll
-    for (int kk = 0; kk < kBK / 2; ++kk) {
+    for (int kk = 0; kk < BK / 2; ++kk) {
       const int k = kk * 2 + (lane >> 5);
-      float fa[2], fb[2];
+      float fa[FM], fb[FN];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) fa[i] = sA[(wm + i * 32 + (lane & 31)) * kPitch + k];
+      for (int i = 0; i < FM; ++i) fa[i] = sA[(wm + i * 32 + (lane & 31)) * P + k];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) fb[j] = sB[(wn + j * 32 + (lane & 31)) * kPitch + k];
+      for (int j = 0; j < FN; ++j) fb[j] = sB[(wn + j * 32 + (lane & 31)) * P + k];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
   }
 
@@ -151,9 +157,9 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(int64_t M, int64_t N
   const int64_t rbase = i0 + wm + 4 * (lane >> 5);
   const int64_t cbase = j0 + wn + (lane & 31);
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < FN; ++j) {
       const int64_t col = cbase + j * 32;
       float* cp = C + (rbase + i * 32) * ldc + col;
       float cv[16];
@@ -176,26 +182,34 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(int64_t M, int64_t N
     }
 }
 
+template <int TM, int TN, int BK>
+int launch_tiles(hipStream_t st, int64_t M, int64_t N, int64_t Kd, float alpha, const Operand& a, const Operand& b,
+                 bool vec, float beta, float* C, int64_t ldc, int flags) {
+  const int tiles_m = static_cast<int>(cdiv(M, TM));
+  const int tiles_n = static_cast<int>(cdiv(N, TN));
+  const dim3 grid(static_cast<unsigned>(tiles_m) * tiles_n);
+  if (vec)
+    hipLaunchKernelGGL((gemm_f32_kernel<TM, TN, BK, true>), grid, dim3(kThreads), 0, st, M, N, Kd, alpha, a, b, beta,
+                       C, ldc, flags, tiles_n);
+  else
+    hipLaunchKernelGGL((gemm_f32_kernel<TM, TN, BK, false>), grid, dim3(kThreads), 0, st, M, N, Kd, alpha, a, b,
+                       beta, C, ldc, flags, tiles_n);
+  return check_launch("gemm_f32");
+}
+
 }  // namespace
 
 int launch_gemm_f32(hipStream_t st, int64_t M, int64_t N, int64_t Kd, float alpha, const float* A, int64_t lda,
                     bool transA, const float* B, int64_t ldb, bool transB, float beta, float* C, int64_t ldc,
                     int flags) {
   if (M <= 0 || N <= 0) return GPTQ_OK;
-  const int tiles_m = static_cast<int>(cdiv(M, kTM));
-  const int tiles_n = static_cast<int>(cdiv(N, kTN));
   Operand a{A, lda, transA, M};
   Operand b{B, ldb, !transB, N};  // operand B is viewed as [j][k]: B^T
   const bool vec = lda % 4 == 0 && ldb % 4 == 0 && (reinterpret_cast<uintptr_t>(A) % 16) == 0 &&
                    (reinterpret_cast<uintptr_t>(B) % 16) == 0;
-  const dim3 grid(static_cast<unsigned>(tiles_m) * tiles_n);
-  if (vec)
-    hipLaunchKernelGGL(gemm_f32_kernel<true>, grid, dim3(kThreads), 0, st, M, N, Kd, alpha, a, b, beta, C, ldc,
-                       flags, tiles_n);
-  else
-    hipLaunchKernelGGL(gemm_f32_kernel<false>, grid, dim3(kThreads), 0, st, M, N, Kd, alpha, a, b, beta, C, ldc,
-                       flags, tiles_n);
-  return check_launch("gemm_f32");
+  if (cdiv(M, 128) * cdiv(N, 128) < 128)
+    return launch_tiles<64, 64, 32>(st, M, N, Kd, alpha, a, b, vec, beta, C, ldc, flags);
+  return launch_tiles<128, 128, 16>(st, M, N, Kd, alpha, a, b, vec, beta, C, ldc, flags);
 }
 
 }  // namespace gptq
