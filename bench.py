@@ -33,6 +33,13 @@ sys.path.insert(0, ROOT)
 METRIC = "s per 8B-shaped block quantized; Hessian MFMA TFLOP/s; W4A16 GEMV HBM GB/s"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
+# Bytes moved below the L2 by the eight Hessian launches of one block at the
+# default workload (262144 tokens), from two rocprofv3 counter passes over
+# this script (FETCH_SIZE, then WRITE_SIZE), calibrated against the
+# hipMemcpy copies of known size in the same runs: read = 1.9975 x FETCH_SIZE
+# KiB, written = 1.0 x WRITE_SIZE KiB (profiles/hessian_llama8b_block_traffic.md).
+HESSIAN_TRAFFIC_TOKENS = 262144
+HESSIAN_TRAFFIC_BYTES = {"read": 380.3e9, "written": 6.8e9}
 
 HID, NQ, NKV, HD, FFN = 4096, 32, 8, 128, 14336
 
@@ -210,6 +217,8 @@ def run_block(args, torch, F, dev):
     wall = time.perf_counter() - t0
     s_per_block = wall / args.steps
     hflops = sum(hessian_flops(n, X.shape[1]) for X in bufs.values())
+    # X read once, H read and written once
+    hbytes = sum(n * X.shape[1] * 2 + 2 * X.shape[1] ** 2 * 4 for X in bufs.values())
     Ks = {k: X.shape[1] for k, X in bufs.items()}
     hms = sum(sum(r["hessian_kernel_ms"].values()) for r in recs) / len(recs)
     per_kernel = {k: sum(r["hessian_kernel_ms"][k] for r in recs) / len(recs) for k in Hs}
@@ -217,7 +226,7 @@ def run_block(args, torch, F, dev):
     losses = {k: float(v.losses_sum.item()) for k, v in res.items()}
     del bufs, Hs, z
     torch.cuda.empty_cache()
-    return dict(s_per_block=s_per_block, wall=wall, hessian_flops=hflops, hessian_ms=hms,
+    return dict(s_per_block=s_per_block, wall=wall, hessian_flops=hflops, hessian_bytes=hbytes, hessian_ms=hms,
                 hessian_kernel_ms=per_kernel, breakdown=breakdown, tokens=n, losses=losses,
                 hessian_tflops_by_key={k: hessian_flops(n, Hs_k) / (per_kernel[k] * 1e-3) / 1e12
                                        for k, Hs_k in Ks.items()},
@@ -365,6 +374,12 @@ def main():
                               "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                               "traffic": None,
                               "work": "n*K*(K+1) flops per Hessian, n = 262144 tokens, K in {4096 x3, 14336}"}
+        if args.nseq * args.seqlen == HESSIAN_TRAFFIC_TOKENS:
+            t = HESSIAN_TRAFFIC_BYTES
+            result["roofline"].update({
+                "traffic": round(t["read"] + t["written"]),
+                "traffic_scope": "bytes per block over the 4 tile + 4 reduce launches, below the L2 (MALL hits included)",
+                "algorithmic_bytes": round(b["hessian_bytes"])})
         result["config"]["forward_attention"] = b["attention"]
         log(f"[bench] block done: {b['s_per_block']:.3f} s/block, Hessian {tflops:.1f} TFLOP/s, {b['breakdown']}, "
             f"by key {b['hessian_tflops_by_key']}, {b['attention']}")

@@ -33,12 +33,39 @@ constexpr int kThreads = 512;
 constexpr int kWaveRows = 128;
 constexpr int kWaveCols = 64;
 
-__device__ __forceinline__ void tile_coords(int t, int& I, int& J) {
+__host__ __device__ __forceinline__ void tile_coords(int t, int& I, int& J) {
   int i = static_cast<int>((sqrtf(8.0f * static_cast<float>(t) + 1.0f) - 1.0f) * 0.5f);
   while ((i + 1) * (i + 2) / 2 <= t) ++i;
   while (i * (i + 1) / 2 > t) --i;
   I = i;
   J = t - i * (i + 1) / 2;
+}
+
+// Tile t of the lower triangle (I >= J) of a T x T tile grid in band order:
+// bands of 4 tile rows, each walked column by column (4 tiles per column left
+// of the diagonal, then the band's own triangle), so that 32 consecutive
+// tiles span 4 row panels and 8 column panels of X.  Bands before band c
+// hold 8c^2 + 2c tiles (only the last band can have fewer than 4 rows).
+__host__ __device__ __forceinline__ void band_coords(int t, int T, int& I, int& J) {
+  int c = static_cast<int>((sqrtf(32.0f * static_cast<float>(t) + 4.0f) - 2.0f) * 0.0625f);
+  while (8 * (c + 1) * (c + 1) + 2 * (c + 1) <= t) ++c;
+  while (8 * c * c + 2 * c > t) --c;
+  const int r0 = 4 * c, h = (T - r0 < 4) ? T - r0 : 4;
+  int u = t - (8 * c * c + 2 * c);
+  if (u < r0 * h) {
+    J = u / h;
+    I = r0 + u % h;
+    return;
+  }
+  u -= r0 * h;
+  int k = 0, len = h;
+  while (u >= len) {
+    u -= len;
+    ++k;
+    --len;
+  }
+  J = r0 + k;
+  I = r0 + k + u;
 }
 
 // LDS slot of feature f: bits 0-2 are XORed with bits 4-6 and with bit 3
@@ -54,10 +81,24 @@ __device__ __forceinline__ int swz(int f) { return f ^ (((f >> 4) ^ ((f >> 1) & 
 // resident on one XCD at a time share one token range and neighbouring
 // feature blocks, which its L2 then serves.
 template <int kMap = 0>
-__device__ __forceinline__ void split_tile(int b, int S, int ntiles, int& s, int& tile) {
+__host__ __device__ __forceinline__ void split_tile(int b, int S, int ntiles, int& s, int& tile) {
   if (kMap == 1) {  // split-major: all XCDs on the same split
     s = b / ntiles;
     tile = b % ntiles;
+    return;
+  }
+  if (kMap == 2) {
+    // split-major over band-ordered tiles, with every round of 256
+    // workgroups (8 XCDs x 32 CUs) permuted so that XCD x runs 32 consecutive
+    // entries of that order: b = 8q + x -> entry 32 (8 (q / 32) + x) + q % 32.
+    // The last partial round keeps b itself.
+    int idx = b;
+    if (b < ((S * ntiles) & ~255)) {
+      const int x = b & 7, q = b >> 3;
+      idx = (((q >> 5) << 3) + x) * 32 + (q & 31);
+    }
+    s = idx / ntiles;
+    tile = idx % ntiles;
     return;
   }
   if (S % 8 == 0) {
@@ -315,9 +356,12 @@ void hessian_dma16(const uint16_t* __restrict__ X, int64_t n, int K, int64_t ldx
   static_assert((2 * kChunks) % kW == 0 && kChunks % kW == 0, "copies split evenly over the waves");
 
   int s, tile;
-  split_tile<kMap>(blockIdx.x, S, ntiles, s, tile);
   int I, J;
-  tile_coords(tile, I, J);
+  split_tile<kMap>(blockIdx.x, S, ntiles, s, tile);
+  if constexpr (kMap == 2)
+    band_coords(tile, static_cast<int>(cdiv(static_cast<int64_t>(K), kTile)), I, J);
+  else
+    tile_coords(tile, I, J);
   const bool diag = (I == J);
   const int nops = diag ? 1 : 2;
   const int bop = diag ? 0 : 1;
@@ -442,7 +486,9 @@ void hessian_dma16(const uint16_t* __restrict__ X, int64_t n, int K, int64_t ldx
 
   // 32x32 accumulator layout: lane l, register v -> row 8*(v/4) + 4*(l/32) + v%4, col l%32
   if (wave_idle) return;
-  float* out = partial + (static_cast<int64_t>(s) * ntiles + tile) * (kTile * kTile);
+  // partials are stored in the row-major triangle order the reduce reads
+  const int slot = I * (I + 1) / 2 + J;
+  float* out = partial + (static_cast<int64_t>(s) * ntiles + slot) * (kTile * kTile);
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -611,11 +657,13 @@ __global__ __launch_bounds__(256) void hessian_reduce(float* __restrict__ H, int
   }
 }
 
+// Token splits: enough for ~2048 workgroups (a multiple of 8, so that the
+// split-major order keeps every XCD on the same split), at most 64, and at
+// least 512 tokens each.
 int choose_splits(int64_t n, int ntiles) {
-  constexpr int kTargetWG = 2048;  // ~8 workgroups per CU on 256 CUs
+  constexpr int kTargetWG = 2048;
   int64_t s = 8 * cdiv(kTargetWG, 8LL * ntiles);
   s = std::min<int64_t>(s, 64);
-  // keep at least 512 tokens per split
   s = std::min<int64_t>(s, std::max<int64_t>(1, n / 512));
   if (s >= 8) s -= s % 8;
   return static_cast<int>(std::max<int64_t>(s, 1));
@@ -662,16 +710,16 @@ extern "C" int gptq_hessian_accumulate(float* H, const void* X, int64_t n, int64
       hipLaunchKernelGGL((hessian_tile32<false>), grid, dim3(kThreads), 0, st, x, n, (int)K, ldx, S, per, ntiles, part);
   } else {
     const uint16_t* x = static_cast<const uint16_t*>(X);
-    // aligned rows: LDS-DMA kernel, 8 waves of 128 x 64, split-major order;
+    // aligned rows: LDS-DMA kernel, 8 waves of 128 x 64, split-major band order;
     // otherwise the register-staged kernel with element loads
     if (dtype == GPTQ_BF16) {
       if (vec)
-        hipLaunchKernelGGL((hessian_dma16<true, 128, 64, 1>), grid, dim3(512), 0, st, x, n, (int)K, ldx, S, per, ntiles, part);
+        hipLaunchKernelGGL((hessian_dma16<true, 128, 64, 2>), grid, dim3(512), 0, st, x, n, (int)K, ldx, S, per, ntiles, part);
       else
         hipLaunchKernelGGL((hessian_tile16<true, false>), grid, dim3(kThreads16), 0, st, x, n, (int)K, ldx, S, per, ntiles, part);
     } else {
       if (vec)
-        hipLaunchKernelGGL((hessian_dma16<false, 128, 64, 1>), grid, dim3(512), 0, st, x, n, (int)K, ldx, S, per, ntiles, part);
+        hipLaunchKernelGGL((hessian_dma16<false, 128, 64, 2>), grid, dim3(512), 0, st, x, n, (int)K, ldx, S, per, ntiles, part);
       else
         hipLaunchKernelGGL((hessian_tile16<false, false>), grid, dim3(kThreads16), 0, st, x, n, (int)K, ldx, S, per, ntiles, part);
     }
