@@ -1,22 +1,22 @@
 // The GPTQ column sweep (quantise, propagate the error) on gfx950.
 //
 // Rows are independent given the read-only propagation matrix T, so the
-// sweep is row-parallel: one wave owns R rows of a sub-block of at most 128
-// columns, lane l holding columns l and l + 64 of every row in registers.
-// Column j is quantised by every lane (only the owner lane's value is
-// final), its error e is broadcast with v_readlane (uniform j, no barrier),
-// and each lane updates its later columns with T[j][col] read from LDS,
-// where the workgroup staged the T sub-block once.
+// sweep is row-parallel: sixteen lanes share a row of a sub-block of at most
+// 128 columns, eight columns each in registers; each column's error is
+// broadcast across the row's lanes with one DPP move and applied at once to
+// the later columns, with T's sub-block staged in LDS once per workgroup.
 //
 // Per block of `blocksize` columns:
 //   1. sweep_params: min-max parameters of every group that starts in the
 //      block, from the weights as they stand at the block start;
-//   2. for each sub-block of <= 128 columns: sweep_sub, then the lazy-batch
+//   2. for each sub-block of <= 128 columns: sweep_r16, then the lazy-batch
 //      update W[:, j2:end] -= E T[j1:j2, j2:end] as one fp32-MFMA GEMM
 //      (end = cols with the trailing update, the block end without it).
 // Splitting a block into sub-blocks with an update in between is an exact
 // re-association of the column-by-column updates.
 #include "gemm.hpp"
+
+#include <utility>
 
 namespace gptq {
 namespace {
@@ -116,120 +116,6 @@ struct SubArgs {
   int64_t e_off;
 };
 
-template <int R, int NC>
-__global__ __launch_bounds__(256) void sweep_sub(SubArgs a) {
-  extern __shared__ float smem[];
-  constexpr int P = 64 * NC;  // pitch of the T sub-block in LDS
-  float* Tb = smem;
-  float* prm = smem + P * P;  // [wave][r][g][2]
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int n = a.n;
-
-  for (int e = tid; e < n * n; e += 256) {
-    const int r = e / n, c = e - (e / n) * n;
-    Tb[r * P + c] = a.T[(a.j1 + r) * a.ldt + a.j1 + c];
-  }
-  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * R;
-  float* wp = prm + wave * (R * a.G * 2);
-  for (int e = lane; e < R * a.G; e += 64) {
-    const int r = e / a.G, g = e - (e / a.G) * a.G;
-    const int64_t row = row0 + r;
-    float s = 1.0f, z = 0.0f;
-    if (row < a.rows) {
-      s = a.scale[row * a.ngroups + a.g_lo + g];
-      z = a.zero[row * a.ngroups + a.g_lo + g];
-    }
-    wp[e * 2] = s;
-    wp[e * 2 + 1] = z;
-  }
-  __syncthreads();
-  if (row0 >= a.rows) return;
-
-  float w[R][NC], qv[R][NC], dv[R][NC], ev[R][NC], lv[R][NC];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int col = c * 64 + lane;
-      const int64_t row = row0 + r;
-      w[r][c] = (row < a.rows && col < n) ? a.W[row * a.cols + a.j1 + col] : 0.0f;
-      qv[r][c] = dv[r][c] = ev[r][c] = lv[r][c] = 0.0f;
-    }
-  float esq[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) esq[r] = 0.0f;
-
-  const float fmaxq = static_cast<float>(a.maxq);
-  for (int j = 0; j < n; ++j) {
-    const int slot = j >> 6;
-    const int owner = j & 63;
-    const int g = a.gs > 0 ? static_cast<int>((a.j1 + j) / a.gs - a.g_lo) : 0;
-    const float d = Tb[j * P + j];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float wj = (NC == 1 || slot == 0) ? w[r][0] : w[r][NC - 1];
-      const float s = wp[(r * a.G + g) * 2];
-      const float z = wp[(r * a.G + g) * 2 + 1];
-      float q;
-      if (a.ref)
-        q = fminf(fmaxf(rintf(wj / s + z), 0.0f), fmaxq);
-      else
-        q = fminf(fmaxf(rintf(wj / s) + z, 0.0f), fmaxq);
-      const float dq = s * (q - z);
-      const float diff = wj - dq;
-      const float e = diff / d;
-      const float eu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), owner));
-      if (lane == owner) {
-        const float loss = diff * diff / (d * d) * 0.5f;
-        if (NC == 1 || slot == 0) {
-          qv[r][0] = q; dv[r][0] = dq; ev[r][0] = e; lv[r][0] = loss;
-        } else {
-          qv[r][NC - 1] = q; dv[r][NC - 1] = dq; ev[r][NC - 1] = e; lv[r][NC - 1] = loss;
-        }
-      }
-      esq[r] += eu * eu;
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int col = c * 64 + lane;
-        if (col > j && col < n) w[r][c] -= eu * Tb[j * P + col];
-      }
-    }
-  }
-
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int64_t row = row0 + r;
-    if (row >= a.rows) continue;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int col = c * 64 + lane;
-      if (col >= n) continue;
-      const int64_t gc = a.j1 + col;
-      const int64_t oc = a.out_cols ? a.out_cols[gc] : gc;
-      a.codes[row * a.cols + oc] = static_cast<uint8_t>(qv[r][c]);
-      if (a.dq) store_elem(a.dq, row * a.cols + oc, a.dq_dtype, dv[r][c]);
-      if (a.losses) a.losses[row * a.cols + oc] = lv[r][c];
-      if (a.Err) a.Err[row * a.lde + a.e_off + col] = ev[r][c];
-    }
-    if (a.err_sq && lane == 0) a.err_sq[row] += esq[r];
-  }
-}
-
-// ------------------------------------------------ lanes-own-rows sweep --
-// Lane = row: every lane quantises its own row, so no work is discarded.  A
-// wave's 64 rows x n (<= 128) columns live column-major in LDS (ws[c][lane],
-// conflict-free); T^T of the sub-block is staged once per workgroup
-// (Tt[c][r] = T[r][c]).  Columns are processed in 32-wide panels: the panel
-// is held in registers and swept with a fully unrolled 32-step loop (T values
-// are LDS broadcast reads), then every later column of the sub-block takes
-// the panel's rank-32 update as a 32-term dot product.
-constexpr int kPW = 32;
-constexpr int kRowWaves = 2;  // waves (64 rows each) per workgroup
-constexpr int kTt = 132;      // row pitch of Tt in floats (16-byte aligned)
-constexpr int kMaxG = 6;      // groups a 128-column sub-block can touch when g >= 32
-
 // a / b from a correctly rounded reciprocal rb of b: one FMA residual step
 // (Markstein), so the quotient is the correctly rounded one except in rare
 // near-midpoint cases, at three dependent operations instead of an IEEE
@@ -240,209 +126,222 @@ __device__ __forceinline__ float div_rcp(float a, float b, float rb) {
   return fmaf(r, rb, q0);
 }
 
+// ------------------------------------------------------ 16-lane sweep --
+// Sixteen lanes per row: lane 16r + q of a wave holds columns 4q..4q+3
+// (registers 0-3) and 64+4q..64+4q+3 (registers 4-7) of row r of the wave's
+// 4 rows.  Column j is quantised by all 16 lanes on the register that holds
+// column j in its owner lane (j < 64: lane j / 4, else (j - 64) / 4), the
+// owner's error is broadcast across the row with one DPP move
+// (row_newbcast), and every lane applies it at once to its later columns: the
+// eager column-by-column update of the GPTQ recurrence, in the same order.
+// A wave covers 4 rows, so a layer of N rows runs as N / 4 waves.
+//
+// The sub-block of T is staged row-major in LDS once per workgroup (a lane
+// reads its coefficients for column j as two 16-byte vectors, consecutive
+// lanes on consecutive vectors), with a per-(column, row) parameter record
+// (scale, zero, 1 / scale of the column's group, 1 / T[j][j]).  Coefficients
+// and parameters are prefetched one column ahead.
+constexpr int kSW = 4;                 // waves per workgroup
+constexpr int kSRows = 4 * kSW;        // rows per workgroup
+constexpr size_t kSweepLds = sizeof(float) * 128 * 128 + sizeof(f32x4) * 128 * kSRows;
+
+struct RowState {
+  float w[8];      // working values of the lane's columns
+  float ev[8];     // errors (owner lanes)
+  uint32_t cq[2];  // codes, 4 per word
+  f32x4 t0, t1;    // T[j][4q..4q+3], T[j][64+4q..+3] of the next column
+  f32x4 pc;        // scale, zero, 1 / scale, 1 / T[j][j] of the next column for this row
+  float d;         // T[j][j] of the next column
+};
+
+// column j: registers 4 (j >= 64) + j % 4, owner lane (j % 64) / 4
+template <int J>
+__device__ __forceinline__ void r16_fetch(RowState& st, const float* Tl, const f32x4* pcol, int q, int rl) {
+  const float* tr = Tl + J * 128;
+  if constexpr (J < 64) st.t0 = *reinterpret_cast<const f32x4*>(tr + 4 * q);
+  st.t1 = *reinterpret_cast<const f32x4*>(tr + 64 + 4 * q);
+  st.pc = pcol[J * kSRows + rl];
+  st.d = tr[J];
+}
+
+template <bool REF, int J>
+__device__ __forceinline__ void r16_step(RowState& st, const float* Tl, const f32x4* pcol, int q, int rl,
+                                         float fmaxq) {
+  constexpr int m = (J >= 64 ? 4 : 0) + (J & 3), q0 = (J & 63) >> 2;
+  const f32x4 t0 = st.t0, t1 = st.t1, pc = st.pc;
+  const float d = st.d;
+  if constexpr (J + 1 < 128) r16_fetch<J + 1>(st, Tl, pcol, q, rl);
+  const float sc = pc[0], z = pc[1], is = pc[2], id = pc[3];
+  const float wj = st.w[m];
+  const float tq = div_rcp(wj, sc, is);
+  float qv;
+  if constexpr (REF)
+    qv = fminf(fmaxf(rintf(tq + z), 0.0f), fmaxq);
+  else
+    qv = fminf(fmaxf(rintf(tq) + z, 0.0f), fmaxq);
+  const float e = div_rcp(wj - sc * (qv - z), d, id);
+  const float eb = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, e), 0x150 + q0, 0xF, 0xF,
+                                                                      false));
+  // registers 0-3 hold columns < 64 (dead once j >= 64); register m first
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = (m + i) & 7;
+    if (J < 64 || r >= 4) st.w[r] = fmaf(-eb, r < 4 ? t0[r] : t1[r - 4], st.w[r]);
+  }
+  // pin the updates to this step (sunk to their next use they would keep
+  // several steps' coefficients live)
+#pragma unroll
+  for (int r = 0; r < 8; ++r) asm volatile("" : "+v"(st.w[r]));
+  const bool own = q == q0;
+  st.ev[m] = own ? e : st.ev[m];
+  st.cq[m >> 2] = own ? st.cq[m >> 2] | (static_cast<uint32_t>(qv) << (8 * (m & 3))) : st.cq[m >> 2];
+  // one step after the other: the next column's loads are in flight, and
+  // nothing later may be hoisted into this step
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <bool REF, int... J>
+__device__ __forceinline__ void r16_steps(RowState& st, const float* Tl, const f32x4* pcol, int q, int rl, float fmaxq,
+                                          std::integer_sequence<int, J...>) {
+  (r16_step<REF, J>(st, Tl, pcol, q, rl, fmaxq), ...);
+}
+
 template <bool REF>
-__global__ __launch_bounds__(64 * kRowWaves) void sweep_rows(SubArgs a) {
+__global__ __launch_bounds__(64 * kSW) void sweep_r16(SubArgs a) {
   extern __shared__ float smem[];
-  float* Tt = smem;                                   // 128 x kTt
-  float* ws_all = smem + 128 * kTt;                   // [wave][128][64]
-  float* prm_all = ws_all + kRowWaves * 128 * 64;     // [wave][kMaxG][2][64]
-  float* invd = prm_all + kRowWaves * kMaxG * 2 * 64;  // [128] 1 / T[j][j]
+  float* Tl = smem;                                          // [128][128] T sub-block, zeros outside
+  f32x4* pcol = reinterpret_cast<f32x4*>(smem + 128 * 128);  // [128][kSRows]
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int q = tid & 15;
+  const int rl = tid >> 4;  // row within the workgroup
   const int n = a.n;
-  float* ws = ws_all + wave * 128 * 64;
-  float* prm = prm_all + wave * kMaxG * 2 * 64;
+  constexpr int kThr = 64 * kSW;
 
-  // Stage the T block transposed (Tt[c][r]) and this lane's row of W (ws),
-  // with eight loads per thread in flight before any is stored: a load-then-
-  // store loop would pay one memory round trip per element.
-  constexpr int kThr = 64 * kRowWaves;
-  constexpr int kBatch = 8;
+  // Stage T (16 vector loads per thread in flight before any is stored).
   const float* tsrc = a.T + a.j1 * a.ldt + a.j1;
-  if ((n & 3) == 0 && (a.ldt & 3) == 0 && (reinterpret_cast<uintptr_t>(tsrc) & 15) == 0) {
-    // vector e covers columns 4 (e / n) .. +3 of row e % n (consecutive
-    // threads, consecutive rows: conflict-free transposed stores)
-    const int tot = n * (n >> 2);
-    for (int e0 = tid; e0 < tot; e0 += kThr * kBatch) {
-      f32x4 v[kBatch];
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int e = e0 + u * kThr;
-        if (e < tot) v[u] = *reinterpret_cast<const f32x4*>(tsrc + (e % n) * a.ldt + 4 * (e / n));
-      }
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int e = e0 + u * kThr;
-        if (e < tot) {
-          const int r = e % n, c = 4 * (e / n);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) Tt[(c + q) * kTt + r] = v[u][q];
-        }
-      }
-    }
-  } else {
-    const int tot = n * n;
-    for (int e0 = tid; e0 < tot; e0 += kThr * kBatch) {
-      float v[kBatch];
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int e = e0 + u * kThr;
-        if (e < tot) v[u] = tsrc[(e % n) * a.ldt + e / n];
-      }
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int e = e0 + u * kThr;
-        if (e < tot) Tt[(e / n) * kTt + e % n] = v[u];
-      }
-    }
-  }
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * (64 * kRowWaves) + wave * 64 + lane;
-  const bool valid = row < a.rows;
-  const int64_t rrow = valid ? row : a.rows - 1;
+  const bool tvec = (n & 3) == 0 && (a.ldt & 3) == 0 && (reinterpret_cast<uintptr_t>(tsrc) & 15) == 0;
   {
-    const float* src = a.W + rrow * a.cols + a.j1;
-    int c = 0;
-    if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {
-      for (; c + 4 * kBatch <= n; c += 4 * kBatch) {
-        f32x4 v[kBatch];
+    f32x4 v[16];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) v[u] = *reinterpret_cast<const f32x4*>(src + c + 4 * u);
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) ws[(c + 4 * u + q) * 64 + lane] = v[u][q];
-      }
-    }
-    for (; c < n; ++c) ws[c * 64 + lane] = src[c];
-  }
-  for (int g = 0; g < a.G; ++g) {
-    prm[(g * 2) * 64 + lane] = a.scale[rrow * a.ngroups + a.g_lo + g];
-    prm[(g * 2 + 1) * 64 + lane] = a.zero[rrow * a.ngroups + a.g_lo + g];
-  }
-  __syncthreads();
-  for (int j = tid; j < n; j += kThr) invd[j] = 1.0f / Tt[j * kTt + j];
-  __syncthreads();
-
-  const float fmaxq = static_cast<float>(a.maxq);
-  const int gs = a.gs;
-  const int j1 = static_cast<int>(a.j1 - a.g_lo * static_cast<int64_t>(gs > 0 ? gs : 0));  // offset in group 0
-  float esq = 0.0f;
-  for (int p0 = 0; p0 < n; p0 += kPW) {
-    // groups of this panel: g0 for columns before `brk`, g0 + 1 after (g >= 32)
-    int g0 = 0, brk = kPW;
-    if (gs > 0) {
-      g0 = (j1 + p0) / gs;
-      brk = (g0 + 1) * gs - (j1 + p0);
-    }
-    const float s0 = prm[(g0 * 2) * 64 + lane], z0 = prm[(g0 * 2 + 1) * 64 + lane];
-    const int g1 = (g0 + 1 < a.G) ? g0 + 1 : g0;
-    const float s1 = prm[(g1 * 2) * 64 + lane], z1 = prm[(g1 * 2 + 1) * 64 + lane];
-    const float is0 = 1.0f / s0, is1 = 1.0f / s1;
-    float ep[kPW], qp[kPW], dp[kPW], lp[kPW];
-#pragma unroll
-    for (int i = 0; i < kPW; ++i) {
-      const int j = p0 + i;
-      ep[i] = qp[i] = dp[i] = lp[i] = 0.0f;
+    for (int u = 0; u < 16; ++u) {
+      const int e = tid + u * kThr, j = e >> 5, c = 4 * (e & 31);
+      v[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       if (j < n) {
-        // left-looking: apply the panel's earlier errors to column j
-        float w = ws[j * 64 + lane];
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        const f32x4* trow = reinterpret_cast<const f32x4*>(Tt + j * kTt + p0);
-#pragma unroll
-        for (int k4 = 0; k4 < (i + 3) / 4; ++k4) {
-          const f32x4 t = trow[k4];
-#pragma unroll
-          for (int u = 0; u < 4; ++u)
-            if (4 * k4 + u < i) acc[u] += ep[4 * k4 + u] * t[u];
-        }
-        w -= (acc[0] + acc[1]) + (acc[2] + acc[3]);
-        const bool second = i >= brk;
-        const float s = second ? s1 : s0;
-        const float is = second ? is1 : is0;
-        const float z = second ? z1 : z0;
-        const float t = div_rcp(w, s, is);
-        float q;
-        if constexpr (REF)
-          q = fminf(fmaxf(rintf(t + z), 0.0f), fmaxq);
-        else
-          q = fminf(fmaxf(rintf(t) + z, 0.0f), fmaxq);
-        const float dq = s * (q - z);
-        const float d = Tt[j * kTt + j];
-        const float diff = w - dq;
-        const float e = div_rcp(diff, d, invd[j]);
-        ep[i] = e;
-        qp[i] = q;
-        dp[i] = dq;
-        lp[i] = 0.5f * e * e;
-        esq += e * e;
-      }
-    }
-    // rank-32 update of the rest of the sub-block
-    for (int c = p0 + kPW; c < n; ++c) {
-      const f32x4* tv = reinterpret_cast<const f32x4*>(Tt + c * kTt + p0);
-      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int v = 0; v < kPW / 4; ++v) {
-        const f32x4 t = tv[v];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) acc[u] += ep[4 * v + u] * t[u];
-      }
-      ws[c * 64 + lane] -= (acc[0] + acc[1]) + (acc[2] + acc[3]);
-    }
-    if (valid) {
-      const int64_t gc0 = a.j1 + p0;
-      const bool full = p0 + kPW <= n;
-      const bool vec = full && !a.out_cols && ((row * a.cols + gc0) & 15) == 0;
-      if (vec) {
-        u32x4 cw[2];
-#pragma unroll
-        for (int v = 0; v < 8; ++v) {
-          const uint32_t w4 = static_cast<uint32_t>(qp[4 * v]) | (static_cast<uint32_t>(qp[4 * v + 1]) << 8) |
-                              (static_cast<uint32_t>(qp[4 * v + 2]) << 16) |
-                              (static_cast<uint32_t>(qp[4 * v + 3]) << 24);
-          cw[v / 4][v % 4] = w4;
-        }
-        u32x4* cdst = reinterpret_cast<u32x4*>(a.codes + row * a.cols + gc0);
-        cdst[0] = cw[0];
-        cdst[1] = cw[1];
-        if (a.losses) {
-          f32x4* ldst = reinterpret_cast<f32x4*>(a.losses + row * a.cols + gc0);
-#pragma unroll
-          for (int v = 0; v < 8; ++v) ldst[v] = f32x4{lp[4 * v], lp[4 * v + 1], lp[4 * v + 2], lp[4 * v + 3]};
-        }
-        if (a.dq) {
-#pragma unroll
-          for (int i = 0; i < kPW; ++i) store_elem(a.dq, row * a.cols + gc0 + i, a.dq_dtype, dp[i]);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < kPW; ++i) {
-          const int j = p0 + i;
-          if (j < n) {
-            const int64_t gc = a.j1 + j;
-            const int64_t oc = a.out_cols ? a.out_cols[gc] : gc;
-            a.codes[row * a.cols + oc] = static_cast<uint8_t>(qp[i]);
-            if (a.dq) store_elem(a.dq, row * a.cols + oc, a.dq_dtype, dp[i]);
-            if (a.losses) a.losses[row * a.cols + oc] = lp[i];
-          }
-        }
-      }
-      if (a.Err) {
-        float* edst = a.Err + row * a.lde + a.e_off + p0;
-        if (full && ((reinterpret_cast<uintptr_t>(edst) & 15) == 0)) {
-#pragma unroll
-          for (int v = 0; v < 8; ++v)
-            reinterpret_cast<f32x4*>(edst)[v] = f32x4{ep[4 * v], ep[4 * v + 1], ep[4 * v + 2], ep[4 * v + 3]};
+        const float* src = tsrc + j * a.ldt + c;
+        if (tvec) {
+          if (c < n) v[u] = *reinterpret_cast<const f32x4*>(src);
         } else {
 #pragma unroll
-          for (int i = 0; i < kPW; ++i)
-            if (p0 + i < n) edst[i] = ep[i];
+          for (int i = 0; i < 4; ++i)
+            if (c + i < n) v[u][i] = src[i];
         }
       }
     }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) reinterpret_cast<f32x4*>(Tl)[tid + u * kThr] = v[u];
   }
-  if (valid && a.err_sq) a.err_sq[row] += esq;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kSRows;
+  const int64_t row = row0 + rl;
+  const int64_t rrow = row < a.rows ? row : a.rows - 1;
+  // this lane's columns of W
+  RowState st;
+  {
+    const float* src = a.W + rrow * a.cols + a.j1;
+    const bool wvec = (n & 3) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = 64 * h + 4 * q;
+      if (wvec) {
+        const f32x4 v = c < n ? *reinterpret_cast<const f32x4*>(src + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) st.w[4 * h + u] = v[u];
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) st.w[4 * h + u] = c + u < n ? src[c + u] : 0.0f;
+      }
+    }
+  }
+  __syncthreads();
+  // parameter records: thread (rl, q) fills columns q, q + 16, ... of its row.
+  // Columns past n get (1, 0, 1, 1): they change no live column (their T
+  // rows are zero) and stay finite.
+  {
+    const int c0 = a.gs > 0 ? static_cast<int>(a.j1 - a.g_lo * a.gs) : 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int c = q + 16 * u;
+      f32x4 r = f32x4{1.0f, 0.0f, 1.0f, 1.0f};
+      if (c < n) {
+        const int g = a.gs > 0 ? (c0 + c) / a.gs : 0;
+        const float sg = a.scale[rrow * a.ngroups + a.g_lo + g];
+        r = f32x4{sg, a.zero[rrow * a.ngroups + a.g_lo + g], 1.0f / sg, 1.0f / Tl[c * 128 + c]};
+      }
+      pcol[c * kSRows + rl] = r;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) st.ev[i] = 0.0f;
+  st.cq[0] = st.cq[1] = 0u;
+  __syncthreads();
+  r16_fetch<0>(st, Tl, pcol, q, rl);
+  r16_steps<REF>(st, Tl, pcol, q, rl, static_cast<float>(a.maxq), std::make_integer_sequence<int, 128>{});
+
+  // row sums of squared errors: lane q's columns, then across the row's 16 lanes
+  float esq = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if ((i < 4 ? 4 * q + i : 60 + 4 * q + i) < n) esq = fmaf(st.ev[i], st.ev[i], esq);
+  esq += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, esq), 0xB1, 0xF, 0xF, false));
+  esq += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, esq), 0x4E, 0xF, 0xF, false));
+  esq += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, esq), 0x141, 0xF, 0xF, false));
+  esq += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, esq), 0x140, 0xF, 0xF, false));
+  if (row >= a.rows) return;
+  if (a.err_sq && q == 0) a.err_sq[row] += esq;
+  const int c0 = a.gs > 0 ? static_cast<int>(a.j1 - a.g_lo * a.gs) : 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = (i < 4 ? 0 : 64) + 4 * q + (i & 3);
+    if (c < n) {
+      const int64_t gc = a.j1 + c;
+      const int64_t oc = a.out_cols ? a.out_cols[gc] : gc;
+      const uint32_t code = (st.cq[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+      a.codes[row * a.cols + oc] = static_cast<uint8_t>(code);
+      if (a.dq) {
+        const int g = a.gs > 0 ? (c0 + c) / a.gs : 0;
+        const float sg = a.scale[row * a.ngroups + a.g_lo + g], zg = a.zero[row * a.ngroups + a.g_lo + g];
+        store_elem(a.dq, row * a.cols + oc, a.dq_dtype, sg * (static_cast<float>(code) - zg));
+      }
+      if (a.losses) a.losses[row * a.cols + oc] = 0.5f * st.ev[i] * st.ev[i];
+      if (a.Err) a.Err[row * a.lde + a.e_off + c] = st.ev[i];
+    }
+  }
+}
+
+// row[perm[c]] = row[c] in place, through LDS: the whole row is read before
+// any of it is written.  Entries of perm outside [0, cols) are skipped.
+constexpr int64_t kUnpermMaxCols = 16384;
+
+template <typename E>
+__device__ __forceinline__ void unpermute_one(E* row, const int32_t* perm, int64_t cols, E* buf) {
+  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+    const uint32_t o = static_cast<uint32_t>(perm[c]);
+    if (o < static_cast<uint64_t>(cols)) buf[o] = row[c];
+  }
+  __syncthreads();
+  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) row[c] = buf[c];
+  __syncthreads();
+}
+
+// one workgroup per row; esz = bytes per dequantised value (0: none)
+__global__ __launch_bounds__(256) void unpermute_rows(uint8_t* __restrict__ codes, void* __restrict__ dq, int esz,
+                                                      float* __restrict__ losses, const int32_t* __restrict__ perm,
+                                                      int64_t cols) {
+  extern __shared__ float ubuf[];
+  const int64_t r = blockIdx.x;
+  unpermute_one(codes + r * cols, perm, cols, reinterpret_cast<uint8_t*>(ubuf));
+  if (esz == 4) unpermute_one(static_cast<float*>(dq) + r * cols, perm, cols, ubuf);
+  if (esz == 2) unpermute_one(static_cast<uint16_t*>(dq) + r * cols, perm, cols, reinterpret_cast<uint16_t*>(ubuf));
+  if (losses) unpermute_one(losses + r * cols, perm, cols, ubuf);
 }
 
 __global__ void fill_zero_f(float* __restrict__ p, int64_t n) {
@@ -491,22 +390,13 @@ __global__ void prepare_weight_k(const void* __restrict__ w, int dtype, int64_t 
   }
 }
 
-int launch_rows(hipStream_t st, const SubArgs& a) {
-  const unsigned blocks = static_cast<unsigned>(cdiv(a.rows, 64LL * kRowWaves));
-  const size_t lds = sizeof(float) * (128 * kTt + kRowWaves * 128 * 64 + kRowWaves * kMaxG * 2 * 64 + 128);
+int launch_r16(hipStream_t st, const SubArgs& a) {
+  const unsigned blocks = static_cast<unsigned>(cdiv(a.rows, kSRows));
   if (a.ref)
-    hipLaunchKernelGGL(sweep_rows<true>, dim3(blocks), dim3(64 * kRowWaves), lds, st, a);
+    hipLaunchKernelGGL(sweep_r16<true>, dim3(blocks), dim3(64 * kSW), kSweepLds, st, a);
   else
-    hipLaunchKernelGGL(sweep_rows<false>, dim3(blocks), dim3(64 * kRowWaves), lds, st, a);
-  return check_launch("sweep_rows");
-}
-
-template <int R, int NC>
-int launch_sub(hipStream_t st, const SubArgs& a) {
-  const unsigned blocks = static_cast<unsigned>(cdiv(a.rows, 4LL * R));
-  const size_t lds = sizeof(float) * (static_cast<size_t>(64 * NC) * (64 * NC) + 4 * R * a.G * 2);
-  hipLaunchKernelGGL((sweep_sub<R, NC>), dim3(blocks), dim3(256), lds, st, a);
-  return check_launch("sweep_sub");
+    hipLaunchKernelGGL(sweep_r16<false>, dim3(blocks), dim3(64 * kSW), kSweepLds, st, a);
+  return check_launch("sweep_r16");
 }
 
 }  // namespace
@@ -594,9 +484,10 @@ extern "C" int gptq_quantize_sweep(float* W, const float* W0, const float* T, in
                        0, st, err_sq, rows);
     if ((rc = check_launch("fill_zero"))) return rc;
   }
-  // rows per wave: more rows per wave amortise the per-column work; fewer
-  // rows give more waves when the layer is narrow
-  const int R = rows >= 4096 ? 4 : (rows >= 1024 ? 2 : 1);
+  // With a column order, codes / dequantised values / losses are written in
+  // sweep order and put in place by one pass per row at the end (scattered
+  // writes from every sub-block would each touch their own cache line).
+  const bool defer = out_cols != nullptr && cols <= kUnpermMaxCols;
   for (int64_t i1 = 0; i1 < cols; i1 += blocksize) {
     const int64_t i2 = std::min<int64_t>(i1 + blocksize, cols);
     if (gs > 0) {
@@ -618,20 +509,9 @@ extern "C" int gptq_quantize_sweep(float* W, const float* W0, const float* T, in
       a.ref = ref ? 1 : 0; a.scale = scale; a.zero = zero; a.ngroups = ngroups;
       a.g_lo = gs > 0 ? j1 / gs : 0;
       a.G = gs > 0 ? static_cast<int>((j2 - 1) / gs - j1 / gs + 1) : 1;
-      a.out_cols = out_cols; a.codes = codes; a.dq = dequant; a.dq_dtype = dequant_dtype;
+      a.out_cols = defer ? nullptr : out_cols; a.codes = codes; a.dq = dequant; a.dq_dtype = dequant_dtype;
       a.err_sq = err_sq; a.losses = losses; a.Err = Err; a.lde = kSub; a.e_off = 0;
-      const bool wide = n > 64;
-      if ((gs <= 0 || gs >= kPW) && a.G <= kMaxG) {
-        // one group boundary at most per 32-column panel
-        rc = launch_rows(st, a);
-      } else if (R == 4) {
-        rc = wide ? launch_sub<4, 2>(st, a) : launch_sub<4, 1>(st, a);
-      } else if (R == 2) {
-        rc = wide ? launch_sub<2, 2>(st, a) : launch_sub<2, 1>(st, a);
-      } else {
-        rc = wide ? launch_sub<1, 2>(st, a) : launch_sub<1, 1>(st, a);
-      }
-      if (rc) return rc;
+      if ((rc = launch_r16(st, a))) return rc;
       const int64_t end = trailing ? cols : i2;
       if (j2 < end) {
         rc = launch_gemm_f32(st, rows, end - j2, n, -1.0f, Err, kSub, false, T + j1 * ldt + j2, ldt, false, 1.0f,
@@ -639,6 +519,11 @@ extern "C" int gptq_quantize_sweep(float* W, const float* W0, const float* T, in
         if (rc) return rc;
       }
     }
+  }
+  if (defer) {
+    hipLaunchKernelGGL(unpermute_rows, dim3(static_cast<unsigned>(rows)), dim3(256), sizeof(float) * cols, st, codes,
+                       dequant, dequant ? dtype_size(dequant_dtype) : 0, losses, out_cols, cols);
+    if ((rc = check_launch("unpermute_rows"))) return rc;
   }
   return GPTQ_OK;
 }

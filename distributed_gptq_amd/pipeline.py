@@ -70,9 +70,11 @@ def _quantize_one(W, U, perm, dead, bits, group_size, blocksize, want_dequant) -
     if gs <= 0:
         scale, zero = _ops.minmax_params(W.float(), bits, -1, 0)
     Wp = _ops.prepare_weight(W, perm=perm, dead=dead)
+    # per-row sums of squared errors instead of the per-weight loss matrix:
+    # sum(losses) = sum((w - q)^2 / d^2) / 2 = sum(err_sq) / 2
     res = _ops.quantize_sweep(Wp, U, bits, gs, blocksize, L.SWEEP_TRAILING, out_cols=perm,
                               dequant_dtype=W.dtype if want_dequant else None, scale=scale, zero=zero,
-                              want_losses=True, want_err=False)
+                              want_losses=False, want_err=True)
     del Wp
     ar = torch.arange(K, device=W.device, dtype=torch.int32)
     gcol = ar // gs if gs > 0 else torch.zeros_like(ar)
@@ -82,7 +84,7 @@ def _quantize_one(W, U, perm, dead, bits, group_size, blocksize, want_dequant) -
         g_idx = torch.empty_like(ar)
         g_idx[perm.long()] = gcol
     return LayerResult(codes=res["codes"], qweight=_ops.pack(res["codes"], bits), scale=res["scale"],
-                       zero=res["zero"], g_idx=g_idx, dequant=res["dequant"], losses_sum=res["losses"].sum())
+                       zero=res["zero"], g_idx=g_idx, dequant=res["dequant"], losses_sum=0.5 * res["err_sq"].sum())
 
 
 class PendingLayers:
