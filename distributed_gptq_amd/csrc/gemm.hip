@@ -4,9 +4,11 @@
 // FM x FN MFMA 32x32 blocks), BK-deep k stages staged in LDS as [row][k]
 // (pitch BK + 2 floats: the two k-rows a 32x32x2 fragment reads land in
 // disjoint bank halves), next stage prefetched into registers while the
-// current one is multiplied.  Large products use 128 x 128 tiles, 16 deep;
-// products that would give fewer than 128 such tiles use 64 x 64 tiles, 32
-// deep (four times the workgroups, half the stages).  Triangular operands
+// current one is multiplied.  Tiles are 128 x 64 (64 x 64 for products that
+// would give fewer than 256 such tiles), 32 deep: small tiles keep enough
+// waves resident per CU to hide the load latency of this single-buffered
+// pipeline, which measured faster than 128 x 128 or 256 x 128 tiles for
+// every product of the factorisation and the sweep.  Triangular operands
 // skip the k-tiles that are known to be zero; GEMM_C_LOWER skips tiles
 // strictly above the diagonal.
 #include "gemm.hpp"
@@ -207,9 +209,9 @@ int launch_gemm_f32(hipStream_t st, int64_t M, int64_t N, int64_t Kd, float alph
   Operand b{B, ldb, !transB, N};  // operand B is viewed as [j][k]: B^T
   const bool vec = lda % 4 == 0 && ldb % 4 == 0 && (reinterpret_cast<uintptr_t>(A) % 16) == 0 &&
                    (reinterpret_cast<uintptr_t>(B) % 16) == 0;
-  if (cdiv(M, 128) * cdiv(N, 128) < 128)
+  if (cdiv(M, 128) * cdiv(N, 64) < 256)
     return launch_tiles<64, 64, 32>(st, M, N, Kd, alpha, a, b, vec, beta, C, ldc, flags);
-  return launch_tiles<128, 128, 16>(st, M, N, Kd, alpha, a, b, vec, beta, C, ldc, flags);
+  return launch_tiles<128, 64, 32>(st, M, N, Kd, alpha, a, b, vec, beta, C, ldc, flags);
 }
 
 }  // namespace gptq

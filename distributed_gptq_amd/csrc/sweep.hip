@@ -11,9 +11,12 @@
 //      block, from the weights as they stand at the block start;
 //   2. for each sub-block of <= 128 columns: sweep_r16, then the lazy-batch
 //      update W[:, j2:end] -= E T[j1:j2, j2:end] as one fp32-MFMA GEMM
-//      (end = cols with the trailing update, the block end without it).
-// Splitting a block into sub-blocks with an update in between is an exact
-// re-association of the column-by-column updates.
+//      (end = the block end without the trailing update; with it, the end of
+//      the run of blocks spanning >= 512 columns that holds the sub-block);
+//   3. with the trailing update, at the end of each run [s1, s2):
+//      W[:, s2:] -= E_run T[s1:s2, s2:] as one GEMM of depth s2 - s1.
+// Both are exact re-associations of the column-by-column updates, and every
+// column has all earlier columns' updates by the time its block starts.
 #include "gemm.hpp"
 
 #include <utility>
@@ -404,11 +407,18 @@ int launch_r16(hipStream_t st, const SubArgs& a) {
 
 using namespace gptq;
 
+// Trailing updates are batched two-level: each sub-block updates the rest of
+// its run of blocks spanning >= kRun columns right away (the columns swept
+// next), and the run's errors update everything after it in one GEMM of
+// depth >= kRun at the run's end.  Errors of a run are kept side by side.
+constexpr int64_t kRun = 512;
+
+int64_t run_blocks(int blocksize) { return std::max<int64_t>(1, cdiv(kRun, blocksize)); }
+
 extern "C" size_t gptq_sweep_workspace_size(int64_t rows, int64_t cols, int blocksize) {
   (void)cols;
-  (void)blocksize;
-  if (rows <= 0) return 0;
-  return static_cast<size_t>(rows) * kSub * sizeof(float);
+  if (rows <= 0 || blocksize <= 0) return 0;
+  return static_cast<size_t>(rows) * std::max<int64_t>(kSub, run_blocks(blocksize) * blocksize) * sizeof(float);
 }
 
 extern "C" int gptq_minmax_params(const float* src, int64_t rows, int64_t cols, int64_t ld, int bits, int group_size,
@@ -488,36 +498,50 @@ extern "C" int gptq_quantize_sweep(float* W, const float* W0, const float* T, in
   // sweep order and put in place by one pass per row at the end (scattered
   // writes from every sub-block would each touch their own cache line).
   const bool defer = out_cols != nullptr && cols <= kUnpermMaxCols;
-  for (int64_t i1 = 0; i1 < cols; i1 += blocksize) {
-    const int64_t i2 = std::min<int64_t>(i1 + blocksize, cols);
-    if (gs > 0) {
-      const int64_t g_first = cdiv(i1, gs);
-      const int64_t g_end = cdiv(i2, gs);  // groups whose start lies in [i1, i2)
-      if (g_end > g_first) {
-        const int64_t g_count = g_end - g_first;
-        const unsigned blocks = static_cast<unsigned>(cdiv(rows * g_count, 4));
-        hipLaunchKernelGGL(sweep_params, dim3(blocks), dim3(256), 0, st, psrc, cols, rows, cols, gs, maxq, ref ? 1 : 0,
-                           g_first, g_count, scale, zero, ngroups);
-        if ((rc = check_launch("sweep_params"))) return rc;
+  // without the trailing update every block stands alone (one Err slot)
+  const int64_t F = trailing ? run_blocks(blocksize) : 1;
+  const int64_t lde = trailing ? std::max<int64_t>(kSub, F * blocksize) : kSub;
+  for (int64_t s1 = 0; s1 < cols; s1 += F * blocksize) {
+    const int64_t s2 = std::min<int64_t>(s1 + F * blocksize, cols);
+    for (int64_t i1 = s1; i1 < s2; i1 += blocksize) {
+      const int64_t i2 = std::min<int64_t>(i1 + blocksize, cols);
+      if (gs > 0) {
+        const int64_t g_first = cdiv(i1, gs);
+        const int64_t g_end = cdiv(i2, gs);  // groups whose start lies in [i1, i2)
+        if (g_end > g_first) {
+          const int64_t g_count = g_end - g_first;
+          const unsigned blocks = static_cast<unsigned>(cdiv(rows * g_count, 4));
+          hipLaunchKernelGGL(sweep_params, dim3(blocks), dim3(256), 0, st, psrc, cols, rows, cols, gs, maxq,
+                             ref ? 1 : 0, g_first, g_count, scale, zero, ngroups);
+          if ((rc = check_launch("sweep_params"))) return rc;
+        }
+      }
+      for (int64_t j1 = i1; j1 < i2; j1 += kSub) {
+        const int64_t j2 = std::min<int64_t>(j1 + kSub, i2);
+        const int n = static_cast<int>(j2 - j1);
+        const int64_t e_off = trailing ? j1 - s1 : 0;
+        SubArgs a;
+        a.W = W; a.T = T; a.ldt = ldt; a.cols = cols; a.rows = rows; a.j1 = j1; a.n = n; a.gs = gs; a.maxq = maxq;
+        a.ref = ref ? 1 : 0; a.scale = scale; a.zero = zero; a.ngroups = ngroups;
+        a.g_lo = gs > 0 ? j1 / gs : 0;
+        a.G = gs > 0 ? static_cast<int>((j2 - 1) / gs - j1 / gs + 1) : 1;
+        a.out_cols = defer ? nullptr : out_cols; a.codes = codes; a.dq = dequant; a.dq_dtype = dequant_dtype;
+        a.err_sq = err_sq; a.losses = losses; a.Err = Err; a.lde = lde; a.e_off = e_off;
+        if ((rc = launch_r16(st, a))) return rc;
+        // the columns swept next: the rest of the run (trailing) or of the block
+        const int64_t end = trailing ? s2 : i2;
+        if (j2 < end) {
+          rc = launch_gemm_f32(st, rows, end - j2, n, -1.0f, Err + e_off, lde, false, T + j1 * ldt + j2, ldt, false,
+                               1.0f, W + j2, cols, 0);
+          if (rc) return rc;
+        }
       }
     }
-    for (int64_t j1 = i1; j1 < i2; j1 += kSub) {
-      const int64_t j2 = std::min<int64_t>(j1 + kSub, i2);
-      const int n = static_cast<int>(j2 - j1);
-      SubArgs a;
-      a.W = W; a.T = T; a.ldt = ldt; a.cols = cols; a.rows = rows; a.j1 = j1; a.n = n; a.gs = gs; a.maxq = maxq;
-      a.ref = ref ? 1 : 0; a.scale = scale; a.zero = zero; a.ngroups = ngroups;
-      a.g_lo = gs > 0 ? j1 / gs : 0;
-      a.G = gs > 0 ? static_cast<int>((j2 - 1) / gs - j1 / gs + 1) : 1;
-      a.out_cols = defer ? nullptr : out_cols; a.codes = codes; a.dq = dequant; a.dq_dtype = dequant_dtype;
-      a.err_sq = err_sq; a.losses = losses; a.Err = Err; a.lde = kSub; a.e_off = 0;
-      if ((rc = launch_r16(st, a))) return rc;
-      const int64_t end = trailing ? cols : i2;
-      if (j2 < end) {
-        rc = launch_gemm_f32(st, rows, end - j2, n, -1.0f, Err, kSub, false, T + j1 * ldt + j2, ldt, false, 1.0f,
-                             W + j2, cols, 0);
-        if (rc) return rc;
-      }
+    // the run's errors, all at once, into every later column
+    if (trailing && s2 < cols) {
+      rc = launch_gemm_f32(st, rows, cols - s2, s2 - s1, -1.0f, Err, lde, false, T + s1 * ldt + s2, ldt, false, 1.0f,
+                           W + s2, cols, 0);
+      if (rc) return rc;
     }
   }
   if (defer) {
