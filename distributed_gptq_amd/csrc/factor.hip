@@ -85,12 +85,12 @@ __global__ void fill_zero(float* __restrict__ p, int64_t n) {
 // One workgroup of 4 waves: Cholesky of the m x m (m <= 128) diagonal block
 // of A at (n0, n0) and the inverse of its factor, blocked by 32:
 //   for each diagonal block k:  one wave factors D_kk = L_kk L_kk^T and
-//     inverts L_kk (X_kk) in registers, broadcasting with v_readlane (no
-//     barriers); then L_ik = A_ik X_kk^T (panel) and A_ij -= L_ik L_jk^T
+//     inverts L_kk (X_kk) together (diag32); then L_ik = A_ik X_kk^T (panel)
+//     and A_ij -= L_ik L_jk^T
 //     (trailing) as 32x32x32 v_mfma_f32_32x32x2f32 products, one per wave;
 //   then X_ij (i > j) = -X_ii sum_{k=j}^{i-1} L_ik X_kj by block distance.
-// The tile is padded to 128 with the identity.  Writes L (zeros above) into
-// A and X = L^-1 (zeros above) into X; a non-positive pivot records
+// The tile is padded to 128 with the identity.  Writes X = L^-1 (zeros
+// above) into X (A's block is left as scratch); a non-positive pivot records
 // info = 1 + (column in A order) once.
 constexpr int kLP = kNB + 1;  // LDS pitch (odd: conflict-free column reads)
 constexpr int kLB = 32;       // diagonal block
@@ -122,44 +122,88 @@ __device__ __forceinline__ void put32(float* pc, int ldc, const f32x16& acc, flo
   for (int v = 0; v < 16; ++v) pc[(8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) * ldc + (lane & 31)] = scale * acc[v];
 }
 
-// One wave: D (32 x 32 at sD) = L L^T in registers (lane r holds row r), L
-// written back over D (zeros above) and X = L^-1 written to sXd (lane c
-// computes column c by forward substitution).
-__device__ __forceinline__ void diag32(float* sD, float* sXd, int lane, int col0, int lim, int& first_bad) {
-  const int r = lane & 31;
-  float a[kLB];
+// Orders one wave's LDS accesses for the compiler: lanes exchange data
+// through LDS, stored by some lanes and read by others, which a single
+// thread's view of memory does not order (wave-scope release and acquire
+// around a wave barrier; the hardware runs a wave's LDS accesses in order).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// One wave: D (32 x 32 at sD, lower part) = L L^T and X = L^-1, written back
+// over D and into sXd (zeros above).  Lane l holds the 4 x 4 sub-block
+// (rows 4 (l / 8) + u, columns 4 (l % 8) + v) of the working matrix and of
+// Y (initially I).  Step j: the pivot comes from its lane (v_readlane); the
+// lanes holding column j store L's column j, the lanes holding row j store
+// Y's row j scaled by 1 / L[j][j], both in LDS (sc, 64 floats), and every
+// lane reads back what it needs and applies the two rank-1 updates
+//   D[r][c] -= L[r][j] L[c][j]  (c > j),   Y[r][c] -= L[r][j] Y[j][c]  (r > j),
+// right-looking Cholesky and forward elimination fused.
+__device__ __forceinline__ void diag32(float* sD, float* sXd, float* sc, int lane, int col0, int lim, int& first_bad) {
+  const int ra = lane >> 3, cb = lane & 7;
+  float a[4][4], y[4][4];
 #pragma unroll
-  for (int c = 0; c < kLB; ++c) a[c] = sD[r * kLP + c];
-  float mydiag = 1.0f;
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      a[u][v] = sD[(4 * ra + u) * kLP + 4 * cb + v];
+      y[u][v] = (4 * ra + u == 4 * cb + v) ? 1.0f : 0.0f;
+    }
+  float* lcol = sc;
+  float* yrow = sc + 32;
 #pragma unroll
   for (int j = 0; j < kLB; ++j) {
-    const float piv = rdl(a[j], j);
+    const int jb = j >> 2, jv = j & 3;
+    const float piv = rdl(a[jv][jv], jb * 8 + jb);
     if (!(piv > 0.0f) && first_bad < 0 && col0 + j < lim) first_bad = col0 + j;
-    const float d = sqrtf(piv);
-    const float inv = 1.0f / d;
-    const float l = (r > j) ? a[j] * inv : (r == j ? d : 0.0f);
-    a[j] = l;
-    if (r == j) mydiag = d;
+    // hardware square root and reciprocal (1 ulp): they sit on the
+    // sequential chain of the 32 steps
+    const float d = __builtin_amdgcn_sqrtf(piv);
+    const float id = __builtin_amdgcn_rcpf(d);
+    if (cb == jb) {
+      f32x4 lv;
 #pragma unroll
-    for (int c = j + 1; c < kLB; ++c) a[c] = fmaf(-l, rdl(l, c), a[c]);
-    __builtin_amdgcn_sched_barrier(0);  // keep the broadcasts of one step together (scalar registers)
+      for (int u = 0; u < 4; ++u) {
+        const int r = 4 * ra + u;
+        lv[u] = r > j ? a[u][jv] * id : (r == j ? d : 0.0f);
+        a[u][jv] = lv[u];
+      }
+      *reinterpret_cast<f32x4*>(lcol + 4 * ra) = lv;
+    }
+    if (ra == jb) {
+      f32x4 yv;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        y[jv][v] *= id;
+        yv[v] = y[jv][v];
+      }
+      *reinterpret_cast<f32x4*>(yrow + 4 * cb) = yv;
+    }
+    wave_sync();
+    const f32x4 lr = *reinterpret_cast<const f32x4*>(lcol + 4 * ra);
+    const f32x4 lc = *reinterpret_cast<const f32x4*>(lcol + 4 * cb);
+    const f32x4 yc = *reinterpret_cast<const f32x4*>(yrow + 4 * cb);
+    wave_sync();
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float lru = 4 * ra + u > j ? lr[u] : 0.0f;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        a[u][v] = fmaf(-lr[u], 4 * cb + v > j ? lc[v] : 0.0f, a[u][v]);
+        y[u][v] = fmaf(-lru, yc[v], y[u][v]);
+      }
+    }
   }
-  const float myinv = 1.0f / mydiag;
-  float x[kLB];
 #pragma unroll
-  for (int rr = 0; rr < kLB; ++rr) {
-    float t = (r == rr) ? 1.0f : 0.0f;
+  for (int u = 0; u < 4; ++u)
 #pragma unroll
-    for (int k = 0; k < rr; ++k) t = fmaf(-rdl(a[k], rr), x[k], t);
-    x[rr] = t * rdl(myinv, rr);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  if (lane < kLB) {
-#pragma unroll
-    for (int c = 0; c < kLB; ++c) sD[r * kLP + c] = (c <= r) ? a[c] : 0.0f;
-#pragma unroll
-    for (int rr = 0; rr < kLB; ++rr) sXd[rr * kLP + r] = x[rr];
-  }
+    for (int v = 0; v < 4; ++v) {
+      const bool low = 4 * ra + u >= 4 * cb + v;
+      sD[(4 * ra + u) * kLP + 4 * cb + v] = low ? a[u][v] : 0.0f;
+      sXd[(4 * ra + u) * kLP + 4 * cb + v] = low ? y[u][v] : 0.0f;
+    }
 }
 
 __global__ __launch_bounds__(256) void chol_inv_leaf(float* __restrict__ A, float* __restrict__ X, int64_t ld,
@@ -173,17 +217,19 @@ __global__ __launch_bounds__(256) void chol_inv_leaf(float* __restrict__ A, floa
   const int wave = tid >> 6;
   constexpr int NB = kNB / kLB;
 
-  // load the lower triangle (identity padding beyond m), eight loads in flight per thread
-  for (int e0 = tid; e0 < kNB * kNB; e0 += 256 * 8) {
-    float v[8];
+  // load the lower triangle (identity padding beyond m), 32 loads in flight per thread
+  for (int e0 = tid; e0 < kNB * kNB; e0 += 256 * 32) {
+    float v[32];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < 32; ++u) {
+      // unconditional loads (clamped into the block), selected afterwards
       const int e = e0 + u * 256;
       const int rr = e >> 7, cc = e & (kNB - 1);
-      v[u] = (rr < m && cc < m && cc <= rr) ? A[(n0 + rr) * ld + n0 + cc] : (rr == cc ? 1.0f : 0.0f);
+      const float t = A[(n0 + min(rr, m - 1)) * ld + n0 + min(cc, m - 1)];
+      v[u] = (rr < m && cc < m && cc <= rr) ? t : (rr == cc ? 1.0f : 0.0f);
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < 32; ++u) {
       const int e = e0 + u * 256;
       sA[(e >> 7) * kLP + (e & (kNB - 1))] = v[u];
       sX[(e >> 7) * kLP + (e & (kNB - 1))] = 0.0f;
@@ -194,7 +240,7 @@ __global__ __launch_bounds__(256) void chol_inv_leaf(float* __restrict__ A, floa
   int first_bad = -1;
   auto blk = [&](float* base, int bi, int bj) { return base + bi * kLB * kLP + bj * kLB; };
   for (int kb = 0; kb < NB; ++kb) {
-    if (wave == 0) diag32(blk(sA, kb, kb), blk(sX, kb, kb), lane, kb * kLB, m, first_bad);
+    if (wave == 0) diag32(blk(sA, kb, kb), blk(sX, kb, kb), sS, lane, kb * kLB, m, first_bad);
     __syncthreads();
     // panel: L_ik = A_ik X_kk^T, one wave per block row
     {
@@ -239,11 +285,13 @@ __global__ __launch_bounds__(256) void chol_inv_leaf(float* __restrict__ A, floa
     __syncthreads();
   }
   if (first_bad >= 0 && tid == 0) atomicCAS(info, 0, static_cast<int32_t>(n0 + first_bad + 1));
-  // write back L and X (lower, zeros above) for the m x m block
-  for (int e = tid; e < m * m; e += 256) {
-    const int rr = e / m, cc = e - (e / m) * m;
-    A[(n0 + rr) * ld + n0 + cc] = (cc <= rr) ? sA[rr * kLP + cc] : 0.0f;
-    X[(n0 + rr) * ld + n0 + cc] = (cc <= rr) ? sX[rr * kLP + cc] : 0.0f;
+  // write back X (lower, zeros above) for the m x m block; L itself is not
+  // needed beyond the leaf (the products above it take X)
+#pragma unroll 8
+  for (int e = tid; e < kNB * kNB; e += 256) {
+    const int rr = e >> 7, cc = e & (kNB - 1);
+    const float v = (cc <= rr) ? sX[rr * kLP + cc] : 0.0f;
+    if (rr < m && cc < m) X[(n0 + rr) * ld + n0 + cc] = v;
   }
 }
 
