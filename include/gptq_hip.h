@@ -104,7 +104,11 @@ int gptq_damp_factor(const float* H, int64_t K, float scale, float percdamp,
  * err_sq (rows, fp32: sum over the row of e^2) and losses (rows x cols fp32,
  * (w - dequant)^2 / T[c][c]^2 / 2).  If out_cols is non-NULL, column c of
  * the sweep is stored at column out_cols[c] of codes/dequant/losses (act-order
- * un-permutation); scale/zero stay in sweep order.
+ * un-permutation); scale/zero stay in sweep order.  out_cols must then be a
+ * permutation of [0, cols).
+ * Workspace: gptq_sweep_workspace_size(rows, cols, blocksize) bytes (the
+ * errors of one run of blocks spanning >= 512 columns: trailing updates are
+ * applied per run, an exact re-association of the per-block updates).
  * Replaces GPTQ.quantize, core/gptq.py:91-214 (column loop :132-194), and the
  * canonical fasterquant loop.
  */

@@ -52,7 +52,9 @@ def test_library_loads_and_reports_version():
     # workspace queries are host-only arithmetic
     assert h.gptq_hessian_workspace_size(65536, 768) > 0
     assert h.gptq_factor_workspace_size(4096) >= 4096 * 4096 * 4
-    assert h.gptq_sweep_workspace_size(4096, 4096, 128) == 4096 * 128 * 4
+    # errors of one run of >= 512 columns (4 blocks of 128; one block of 1024)
+    assert h.gptq_sweep_workspace_size(4096, 4096, 128) == 4096 * 512 * 4
+    assert h.gptq_sweep_workspace_size(4096, 4096, 1024) == 4096 * 1024 * 4
 
 
 def test_entry_points_reject_bad_arguments_without_gpu():
