@@ -33,13 +33,12 @@ sys.path.insert(0, ROOT)
 METRIC = "s per 8B-shaped block quantized; Hessian MFMA TFLOP/s; W4A16 GEMV HBM GB/s"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
-# Bytes moved below the L2 by the eight Hessian launches of one block at the
-# default workload (262144 tokens), from two rocprofv3 counter passes over
-# this script (FETCH_SIZE, then WRITE_SIZE), calibrated against the
-# hipMemcpy copies of known size in the same runs: read = 1.9975 x FETCH_SIZE
-# KiB, written = 1.0 x WRITE_SIZE KiB (profiles/hessian_llama8b_block_traffic.md).
-HESSIAN_TRAFFIC_TOKENS = 262144
-HESSIAN_TRAFFIC_BYTES = {"read": 380.3e9, "written": 6.8e9}
+# Bytes moved below the L2 by the down_proj Hessian's tile + reduce launches
+# (the roofline's kernel, run alone over 262144 tokens), from two rocprofv3
+# counter passes over this script (FETCH_SIZE, then WRITE_SIZE), calibrated
+# against the hipMemcpy copies of known size in the same runs
+# (profiles/hessian_llama8b_block_traffic.md).
+HESSIAN_TRAFFIC = {"tokens": 262144, "read": None, "written": None}
 
 HID, NQ, NKV, HD, FFN = 4096, 32, 8, 128, 14336
 
@@ -115,12 +114,13 @@ class Block:
             v = v.repeat_interleave(NQ // NKV, dim=1)
             return F.scaled_dot_product_attention(q, k, v, is_causal=True)
 
-    def collect(self, torch, F, z, bufs, chunk, cos, sin):
-        """Forward over all sequences; store the four layer inputs (written
-        in place into their calibration buffers)."""
+    def collect(self, torch, F, z, bufs, chunk, cos, sin, seqs=None):
+        """Forward over sequences [s_begin, s_end) (all by default); store the
+        four layer inputs (written in place into their calibration buffers)."""
         nseq, T, _ = z.shape
         c, s_ = cos[:, None], sin[:, None]
-        for s0 in range(0, nseq, chunk):
+        s_begin, s_end = seqs if seqs is not None else (0, nseq)
+        for s0 in range(s_begin, s_end, chunk):
             zc = z[s0:s0 + chunk]
             b = zc.shape[0]
             r0, r1 = s0 * T, (s0 + b) * T
@@ -159,26 +159,27 @@ def run_block(args, torch, F, dev):
     cos, sin = blk.rope(torch, T, dev)
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
 
-    # The down_proj chain (largest K) is the critical path: its Hessian is
-    # built first and its factorisation/sweep starts on a side stream while
-    # the other three Hessians are built on the main stream and their chains
-    # start on three more side streams.
-    pool = pipeline.side_streams(dev, 4)
+    # The forward runs in `groups` groups of sequences; each group's four
+    # Hessian accumulations go to a dedicated stream while the next group's
+    # forward runs on the main stream (H += X_g^T X_g, the reference's
+    # per-batch add_batch).  The down_proj chain (largest K) is the critical
+    # path: after the last group its Hessian is finished first and its
+    # factorisation / sweep start on a side stream, then the other three
+    # Hessians finish and their chains start on three more side streams.
+    pool = pipeline.side_streams(dev, 5)
+    G = max(1, min(args.hessian_groups, nseq))
+    # one group: the Hessians follow the forward on the main stream
+    hst, pool = (pool[4] if G > 1 else torch.cuda.current_stream(dev)), pool[:4]
     first = "down"
+    order = [first] + [k for k in Hs if k != first]
     names = {k: [n for n in blk.w if blk.hkey[n] == k] for k in Hs}
+    bounds = [(g * nseq // G, (g + 1) * nseq // G) for g in range(G)]
 
     def step(record):
         e = [ev() for _ in range(4)]
-        he = {k: (ev(), ev()) for k in Hs}
+        he = {k: [] for k in Hs}
+        main = torch.cuda.current_stream(dev)
         e[0].record()
-        blk.collect(torch, F, z, bufs, args.chunk, cos, sin)
-        e[1].record()
-
-        def hessian(k):
-            Hs[k].zero_()
-            he[k][0].record()
-            _ops.hessian_accumulate(Hs[k], bufs[k])
-            he[k][1].record()
 
         def start(keys, streams):
             w = {n: blk.w[n] for k in keys for n in names[k]}
@@ -186,13 +187,30 @@ def run_block(args, torch, F, dev):
                                                   group_size=128, blocksize=128, percdamp=0.01, actorder=True,
                                                   want_dequant=True, check=True, streams=streams)
 
-        hessian(first)
-        p_first = start([first], pool[:1])
-        rest = [k for k in Hs if k != first]
-        for k in rest:
-            hessian(k)
-        e[2].record()
-        p_rest = start(rest, pool[1:])
+        hst.wait_stream(main)  # the previous step's chains have read H
+        with torch.cuda.stream(hst):
+            for k in order:
+                Hs[k].zero_()
+        p_first = p_rest = None
+        for gi, (s0, s1) in enumerate(bounds):
+            blk.collect(torch, F, z, bufs, args.chunk, cos, sin, seqs=(s0, s1))
+            hst.wait_stream(main)
+            last = gi == G - 1
+            if last:
+                e[1].record()
+            with torch.cuda.stream(hst):
+                for k in order:
+                    a, b = ev(), ev()
+                    a.record()
+                    _ops.hessian_accumulate(Hs[k], bufs[k][s0 * T:s1 * T])
+                    b.record()
+                    he[k].append((a, b))
+                    if last and k == first:
+                        p_first = start([first], pool[:1])
+                if last:
+                    e[2].record()
+                    p_rest = start(order[1:], pool[1:])
+        main.wait_stream(hst)
         done = {**p_first.wait(), **p_rest.wait()}
         res = {n: done[n] for n in blk.w}
         e[3].record()
@@ -202,7 +220,7 @@ def run_block(args, torch, F, dev):
                 "forward_ms": e[0].elapsed_time(e[1]),
                 "hessian_ms": e[1].elapsed_time(e[2]),
                 "quantize_ms": e[2].elapsed_time(e[3]),
-                "hessian_kernel_ms": {k: he[k][0].elapsed_time(he[k][1]) for k in he},
+                "hessian_kernel_ms": {k: sum(a.elapsed_time(b) for a, b in he[k]) for k in he},
             })
         return res
 
@@ -224,9 +242,24 @@ def run_block(args, torch, F, dev):
     per_kernel = {k: sum(r["hessian_kernel_ms"][k] for r in recs) / len(recs) for k in Hs}
     breakdown = {k: round(sum(r[k] for r in recs) / len(recs), 3) for k in ("forward_ms", "hessian_ms", "quantize_ms")}
     losses = {k: float(v.losses_sum.item()) for k, v in res.items()}
+    # the dominant kernel alone: the down_proj Hessian over all tokens (the
+    # block's own calibration data), timed on its stream
+    iso = []
+    for _ in range(2):
+        a, b = ev(), ev()
+        Hs[first].zero_()
+        a.record()
+        _ops.hessian_accumulate(Hs[first], bufs[first])
+        b.record()
+        torch.cuda.synchronize()
+        iso.append(a.elapsed_time(b))
+    iso_ms = min(iso)
+    iso_flops = hessian_flops(n, bufs[first].shape[1])
+    iso_bytes = n * bufs[first].shape[1] * 2 + 2 * bufs[first].shape[1] ** 2 * 4
     del bufs, Hs, z
     torch.cuda.empty_cache()
     return dict(s_per_block=s_per_block, wall=wall, hessian_flops=hflops, hessian_bytes=hbytes, hessian_ms=hms,
+                hessian_iso_ms=iso_ms, hessian_iso_flops=iso_flops, hessian_iso_bytes=iso_bytes, groups=G,
                 hessian_kernel_ms=per_kernel, breakdown=breakdown, tokens=n, losses=losses,
                 hessian_tflops_by_key={k: hessian_flops(n, Hs_k) / (per_kernel[k] * 1e-3) / 1e12
                                        for k, Hs_k in Ks.items()},
@@ -338,6 +371,8 @@ def main():
     ap.add_argument("--nseq", type=int, default=128)
     ap.add_argument("--seqlen", type=int, default=2048)
     ap.add_argument("--chunk", type=int, default=8, help="sequences per forward chunk")
+    ap.add_argument("--hessian-groups", type=int, default=1,
+                    help="forward groups whose Hessian accumulation overlaps the next group's forward")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
     ap.add_argument("--no-block", action="store_true")
@@ -363,26 +398,29 @@ def main():
     if not args.no_block:
         log(f"[bench] block: {args.nseq} x {args.seqlen} tokens, warmup {args.warmup}, steps {args.steps}")
         b = run_block(args, torch, F, dev)
-        tflops = b["hessian_flops"] / (b["hessian_ms"] * 1e-3) / 1e12
+        tflops_blk = b["hessian_flops"] / (b["hessian_ms"] * 1e-3) / 1e12
+        tflops = b["hessian_iso_flops"] / (b["hessian_iso_ms"] * 1e-3) / 1e12
         result.update({"value": round(b["s_per_block"], 4), "unit": "s/block",
                        "ms_per_step": round(b["s_per_block"] * 1e3, 2),
-                       "hessian_tflops": round(tflops, 1), "breakdown_ms": b["breakdown"],
-                       "hessian_kernel_ms": {k: round(v, 3) for k, v in b["hessian_kernel_ms"].items()},
-                       "hessian_tflops_by_key": {k: round(v, 1) for k, v in b["hessian_tflops_by_key"].items()},
+                       "hessian_groups": b["groups"], "breakdown_ms": b["breakdown"],
+                       "hessian_tflops_in_block": round(tflops_blk, 1),
+                       "hessian_kernel_ms_in_block": {k: round(v, 3) for k, v in b["hessian_kernel_ms"].items()},
                        "layer_losses": {k: round(v, 4) for k, v in b["losses"].items()}})
-        result["roofline"] = {"bound": "mfma", "kernel": "hessian (tile + reduce)", "achieved": round(tflops, 1),
-                              "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-                              "traffic": None,
-                              "work": "n*K*(K+1) flops per Hessian, n = 262144 tokens, K in {4096 x3, 14336}"}
-        if args.nseq * args.seqlen == HESSIAN_TRAFFIC_TOKENS:
-            t = HESSIAN_TRAFFIC_BYTES
+        result["roofline"] = {"bound": "mfma", "kernel": "hessian_dma16 + hessian_reduce (down_proj input, alone)",
+                              "achieved": round(tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                              "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                              "launch_ms": round(b["hessian_iso_ms"], 3),
+                              "work": f"n*K*(K+1) flops, n = {args.nseq * args.seqlen} tokens, K = {FFN}"}
+        if args.nseq * args.seqlen == HESSIAN_TRAFFIC["tokens"] and HESSIAN_TRAFFIC["read"] is not None:
+            t = HESSIAN_TRAFFIC
             result["roofline"].update({
                 "traffic": round(t["read"] + t["written"]),
-                "traffic_scope": "bytes per block over the 4 tile + 4 reduce launches, below the L2 (MALL hits included)",
-                "algorithmic_bytes": round(b["hessian_bytes"])})
+                "traffic_scope": "bytes per tile + reduce launch pair, below the L2 (MALL hits included)",
+                "algorithmic_bytes": round(b["hessian_iso_bytes"])})
         result["config"]["forward_attention"] = b["attention"]
-        log(f"[bench] block done: {b['s_per_block']:.3f} s/block, Hessian {tflops:.1f} TFLOP/s, {b['breakdown']}, "
-            f"by key {b['hessian_tflops_by_key']}, {b['attention']}")
+        log(f"[bench] block done: {b['s_per_block']:.3f} s/block, groups {b['groups']}, {b['breakdown']}, "
+            f"Hessian in block {tflops_blk:.1f} TFLOP/s, down_proj Hessian alone {tflops:.1f} TFLOP/s, "
+            f"{b['attention']}")
     if not args.no_gemv:
         g4, agg4 = run_gemv(args, torch, dev, 4)
         log(f"[bench] W4A16 GEMV: {g4}")
