@@ -166,10 +166,14 @@ def run_block(args, torch, F, dev):
     # path: after the last group its Hessian is finished first and its
     # factorisation / sweep start on a side stream, then the other three
     # Hessians finish and their chains start on three more side streams.
-    pool = pipeline.side_streams(dev, 5)
+    # Three side streams plus the main stream fill the 4 hardware queues HIP
+    # uses by default (a fifth stream would share a queue and serialise): the
+    # down_proj chain, the gate/up chain, the q/k/v chain, and the o_proj
+    # chain on the main stream after the Hessians.
+    pool = pipeline.side_streams(dev, 4)
     G = max(1, min(args.hessian_groups, nseq))
     # one group: the Hessians follow the forward on the main stream
-    hst, pool = (pool[4] if G > 1 else torch.cuda.current_stream(dev)), pool[:4]
+    hst, pool = (pool[3] if G > 1 else torch.cuda.current_stream(dev)), pool[:3]
     first = "down"
     order = [first] + [k for k in Hs if k != first]
     names = {k: [n for n in blk.w if blk.hkey[n] == k] for k in Hs}
@@ -209,7 +213,7 @@ def run_block(args, torch, F, dev):
                         p_first = start([first], pool[:1])
                 if last:
                     e[2].record()
-                    p_rest = start(order[1:], pool[1:])
+                    p_rest = start(order[1:], [pool[1], pool[2], hst])
         main.wait_stream(hst)
         done = {**p_first.wait(), **p_rest.wait()}
         res = {n: done[n] for n in blk.w}

@@ -55,7 +55,10 @@ _SIDE_STREAMS: Dict[int, list] = {}
 
 
 def side_streams(device: torch.device, n: int) -> list:
-    """``n`` reusable streams of the default priority on ``device``."""
+    """``n`` reusable streams of the default priority on ``device``.  HIP maps
+    streams onto GPU_MAX_HW_QUEUES hardware queues (4 by default), so the
+    caller's stream plus more than three side streams put two streams on one
+    queue, whose work then runs one after the other."""
     idx = torch.device(device).index
     pool = _SIDE_STREAMS.setdefault(idx, [])
     while len(pool) < n:
@@ -110,7 +113,7 @@ def quantize_layers_async(weights: Dict[str, torch.Tensor], hkeys: Dict[str, str
                           hessians: Dict[str, Tuple[torch.Tensor, int]], bits: int = 4, group_size: int = 128,
                           blocksize: int = 128, percdamp: float = 0.01, actorder: bool = False,
                           want_dequant: bool = True, check: bool = True,
-                          streams: Union[int, Sequence[torch.cuda.Stream]] = 4) -> PendingLayers:
+                          streams: Union[int, Sequence[torch.cuda.Stream]] = 3) -> PendingLayers:
     """Starts GPTQ (canonical) on every layer in ``weights`` (name -> (N, K)
     weight) with Hessian ``hessians[hkeys[name]]`` = (sum x x^T, nsamples):
     each Hessian's chain on one of ``streams`` (a count taken from a reusable
@@ -146,7 +149,7 @@ def quantize_layers(weights: Dict[str, torch.Tensor], hkeys: Dict[str, str],
                     hessians: Dict[str, Tuple[torch.Tensor, int]], bits: int = 4, group_size: int = 128,
                     blocksize: int = 128, percdamp: float = 0.01, actorder: bool = False,
                     want_dequant: bool = True, check: bool = True,
-                    streams: Union[int, Sequence[torch.cuda.Stream]] = 4) -> Dict[str, LayerResult]:
+                    streams: Union[int, Sequence[torch.cuda.Stream]] = 3) -> Dict[str, LayerResult]:
     """GPTQ (canonical) on every layer in ``weights`` (name -> (N, K) weight),
     with Hessian ``hessians[hkeys[name]]`` = (sum x x^T, nsamples).  Results
     are ordered after the caller's current stream on return."""
