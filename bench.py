@@ -314,6 +314,8 @@ def run_gemv(args, torch, dev, bits, M=1, min_bytes=1 << 30, reps=3):
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / (reps * R)
         out[f"{N}x{K}"] = {"us": round(us, 3), "GBps": round(nbytes / us * 1e-3, 1), "bytes": nbytes, "buffers": R}
+        if M > 1:
+            out[f"{N}x{K}"]["TFLOPs"] = round(2.0 * M * N * K / us * 1e-6, 1)
         del qs, sc, graph
         torch.cuda.empty_cache()
     tot_b = sum(v["bytes"] for v in out.values())
@@ -380,6 +382,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
     ap.add_argument("--no-block", action="store_true")
+    ap.add_argument("--no-3bit", action="store_true", help="skip the 3-bit block run")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -422,6 +425,13 @@ def main():
                 "traffic_scope": "bytes per tile + reduce launch pair, below the L2 (MALL hits included)",
                 "algorithmic_bytes": round(b["hessian_iso_bytes"])})
         result["config"]["forward_attention"] = b["attention"]
+        if args.bits == 4 and not args.no_3bit:
+            # the same block at 3 bits (g128, act-order): a second configuration of the workload
+            a3 = argparse.Namespace(**{**vars(args), "bits": 3, "steps": max(1, min(args.steps, 2))})
+            b3 = run_block(a3, torch, F, dev)
+            result["block_3bit"] = {"s_per_block": round(b3["s_per_block"], 4), "breakdown_ms": b3["breakdown"],
+                                    "layer_losses": {k: round(v, 4) for k, v in b3["losses"].items()}}
+            log(f"[bench] 3-bit block: {b3['s_per_block']:.3f} s/block, {b3['breakdown']}")
         log(f"[bench] block done: {b['s_per_block']:.3f} s/block, groups {b['groups']}, {b['breakdown']}, "
             f"Hessian in block {tflops_blk:.1f} TFLOP/s, down_proj Hessian alone {tflops:.1f} TFLOP/s, "
             f"{b['attention']}")
@@ -434,6 +444,12 @@ def main():
         result["w3a16_gemv_gbps"] = round(agg3, 1)
         result["gemv"] = {"w4a16_m1": g4, "w3a16_m1": g3, "peak_GBps": PEAK_HBM_GBS,
                           "w4a16_frac": round(agg4 / PEAK_HBM_GBS, 4)}
+        # batched activations (the dequant-GEMM path), M = 16 and 128
+        for bits in (4, 3):
+            for M in (16, 128):
+                gm, _ = run_gemv(args, torch, dev, bits, M=M)
+                result["gemv"][f"w{bits}a16_m{M}"] = gm
+                log(f"[bench] W{bits}A16 M={M}: {gm}")
     if args.no_block:
         result.setdefault("value", None)
     if not args.no_cpu:

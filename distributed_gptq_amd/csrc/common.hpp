@@ -78,4 +78,14 @@ inline bool valid_dtype(int d) { return d == GPTQ_F32 || d == GPTQ_F16 || d == G
 inline int dtype_size(int d) { return d == GPTQ_F32 ? 4 : 2; }
 __host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Orders one wave's LDS accesses for the compiler: lanes exchange data
+// through LDS, stored by some lanes and read by others, which a single
+// thread's view of memory does not order (wave-scope release and acquire
+// around a wave barrier; the hardware runs a wave's LDS accesses in order).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 }  // namespace gptq

@@ -122,16 +122,6 @@ __device__ __forceinline__ void put32(float* pc, int ldc, const f32x16& acc, flo
   for (int v = 0; v < 16; ++v) pc[(8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) * ldc + (lane & 31)] = scale * acc[v];
 }
 
-// Orders one wave's LDS accesses for the compiler: lanes exchange data
-// through LDS, stored by some lanes and read by others, which a single
-// thread's view of memory does not order (wave-scope release and acquire
-// around a wave barrier; the hardware runs a wave's LDS accesses in order).
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // One wave: D (32 x 32 at sD, lower part) = L L^T and X = L^-1, written back
 // over D and into sXd (zeros above).  Lane l holds the 4 x 4 sub-block
 // (rows 4 (l / 8) + u, columns 4 (l % 8) + v) of the working matrix and of

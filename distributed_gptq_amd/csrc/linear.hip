@@ -716,6 +716,420 @@ __global__ __launch_bounds__(256) void dq_mfma_k(LinArgs a) {
   }
 }
 
+// --------------------------------------------- dequant GEMM (M > 4) ----
+// Y (M x N) = X (M x K) W^T with W = s (q - z) dequantised on the fly into
+// the activation type, as the reference dequantises its packed weights to the
+// layer dtype before multiplying (one rounding of the exact product (q - z) s).
+// One workgroup computes NT weight rows x MT activation rows; its WAVES waves
+// split K into 128-column blocks taken round-robin (block b by wave b % WAVES),
+// so each wave's serial chain is K / (128 WAVES) blocks long, and the waves'
+// partial tiles are summed through LDS at the end (fixed order).  Per block a
+// lane loads 32-code chunks (16 bytes at 4 bits) and their group's scale and
+// zero, dequantises them into the wave's own LDS tile, and the wave
+// multiplies 16 x 16 x 32 MFMA fragments: W from that tile, X straight from
+// memory.  The next block's codes and X are in flight while the current
+// block is multiplied.
+template <int NT, int MT, int WAVES>
+struct DsCfg {
+  static constexpr int BN = NT / 16, BM = MT / 16;  // 16-row blocks of W and X
+  static constexpr int CPL = NT / 16;               // 32-code chunks per lane and block
+  static constexpr int P = 128 + 8;                 // LDS tile row pitch (halves)
+  static constexpr size_t kTile = static_cast<size_t>(NT) * P * 2;
+  static constexpr size_t kLds = WAVES * kTile + static_cast<size_t>(NT) * MT * 4;
+};
+
+// the 32 codes of a chunk as 16 pairs (codes 2p, 2p + 1 in the low / high halves)
+template <int BITS, int PP>
+__device__ __forceinline__ uint32_t chunk_pair(const uint32_t (&w)[BITS]) {
+  if constexpr (BITS == 4) {
+    const uint32_t v = (w[PP / 4] >> (8 * (PP % 4))) & 0xFFu;
+    return (v & 0xFu) | ((v >> 4) << 16);
+  } else if constexpr (BITS == 2) {
+    const uint32_t v = (w[PP / 8] >> (4 * (PP % 8))) & 0xFu;
+    return (v & 0x3u) | ((v >> 2) << 16);
+  } else if constexpr (BITS == 8) {
+    const uint32_t v = w[PP / 2] >> (16 * (PP % 2));
+    return (v & 0xFFu) | ((v & 0xFF00u) << 8);
+  } else {
+    constexpr int b0 = 6 * PP, d = b0 / 32, o = b0 % 32;
+    uint64_t v = w[d];
+    if constexpr (d + 1 < 3) v |= static_cast<uint64_t>(w[d + 1]) << 32;
+    v >>= o;
+    return static_cast<uint32_t>(v & 7u) | (static_cast<uint32_t>((v >> 3) & 7u) << 16);
+  }
+}
+
+// dequantised pair (exact (q - z), one rounding of the product by s), fp32 arithmetic
+template <bool BF16>
+__device__ __forceinline__ uint32_t dq_pair(uint32_t c, float s, float z) {
+  const float lo = (static_cast<float>(c & 0xFFFFu) - z) * s;
+  const float hi = (static_cast<float>(c >> 16) - z) * s;
+  if constexpr (BF16) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+  } else {
+    return __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(lo), static_cast<_Float16>(hi)});
+  }
+}
+
+// the same for fp16 with an integer zero in [0, 1023]: packed fp16, where
+// (1024 + q) - (1024 + z) is exact
+__device__ __forceinline__ uint32_t dq_pair16(uint32_t c, uint32_t zz, uint32_t sh) {
+  const f16x2 h = __builtin_bit_cast(f16x2, c | 0x64006400u) - __builtin_bit_cast(f16x2, zz);
+  return __builtin_bit_cast(uint32_t, h * __builtin_bit_cast(f16x2, sh));
+}
+
+template <int BITS, bool BF16, int... PP>
+__device__ __forceinline__ void dq_chunk(const uint32_t (&cw)[BITS], float s, float z, uint32_t (&d)[16],
+                                         std::integer_sequence<int, PP...>) {
+  if constexpr (!BF16) {
+    // GPTQ zero points are integers: the packed path, chosen for the whole wave
+    if (__all(z == rintf(z) && z >= 0.0f && z <= 1023.0f)) {
+      const uint32_t zz = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(1024.0f + z),
+                                                              static_cast<_Float16>(1024.0f + z)});
+      const uint32_t sh = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(s), static_cast<_Float16>(s)});
+      ((d[PP] = dq_pair16(chunk_pair<BITS, PP>(cw), zz, sh)), ...);
+      return;
+    }
+  }
+  ((d[PP] = dq_pair<BF16>(chunk_pair<BITS, PP>(cw), s, z)), ...);
+}
+
+// one 128-column block of a wave: codes, scales and zeros of its rows, and
+// (for a single 16-row X block) its X fragments; with more X blocks the
+// fragments are loaded one 32-column step ahead inside the block instead
+template <int BITS, int NT, int MT>
+struct DsBlock {
+  static constexpr int XB = MT == 16 ? 4 : 1;
+  uint32_t cw[NT / 16][BITS];
+  float s[NT / 16], z[NT / 16];
+  uint4 x[XB][MT / 16];
+};
+
+template <int BITS, bool BF16, int NT, int MT, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void dq_split_k(LinArgs a) {
+  using C = DsCfg<NT, MT, WAVES>;
+  constexpr int BN = C::BN, BM = C::BM, P = C::P;
+  extern __shared__ __attribute__((aligned(16))) uint16_t dsm[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  uint16_t* tile = dsm + wave * (NT * P);
+  float* red = reinterpret_cast<float*>(dsm + WAVES * NT * P);
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * NT;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * MT;
+  const int nblk = static_cast<int>(a.K / 128);
+  const int r16 = lane & 15, oct = lane >> 4;
+
+  const uint8_t* wrow[BN];
+  int64_t wn[BN];
+#pragma unroll
+  for (int i = 0; i < BN; ++i) {
+    wn[i] = std::min<int64_t>(n0 + 16 * i + r16, a.N - 1);
+    wrow[i] = a.packed + wn[i] * a.pitch;
+  }
+  // X row of B-fragment block j (rows past M read as zeros)
+  const uint16_t* xrow[BM];
+  bool xok[BM];
+#pragma unroll
+  for (int j = 0; j < BM; ++j) {
+    const int64_t m = m0 + 16 * j + r16;
+    xok[j] = m < a.M;
+    xrow[j] = a.x + (xok[j] ? m : 0) * a.K;
+  }
+
+  auto loadx = [&](int b, int kk, int j) {
+    return xok[j] ? *reinterpret_cast<const uint4*>(xrow[j] + static_cast<int64_t>(b) * 128 + 32 * kk + 8 * oct)
+                  : uint4{0u, 0u, 0u, 0u};
+  };
+  // lane (r16, oct): chunk oct (codes 32 oct .. + 31 of the block) of rows 16 i + r16
+  auto load = [&](int b, DsBlock<BITS, NT, MT>& L) {
+    const int64_t k = static_cast<int64_t>(b) * 128 + 32 * oct;
+    const int64_t g = k / a.gs;
+#pragma unroll
+    for (int i = 0; i < BN; ++i) {
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(wrow[i] + k * BITS / 8);
+      if constexpr (BITS == 4) {
+        const uint4 v = *reinterpret_cast<const uint4*>(src);
+        L.cw[i][0] = v.x; L.cw[i][1] = v.y; L.cw[i][2] = v.z; L.cw[i][3] = v.w;
+      } else if constexpr (BITS == 8) {
+        const uint4 v0 = reinterpret_cast<const uint4*>(src)[0], v1 = reinterpret_cast<const uint4*>(src)[1];
+        L.cw[i][0] = v0.x; L.cw[i][1] = v0.y; L.cw[i][2] = v0.z; L.cw[i][3] = v0.w;
+        L.cw[i][4] = v1.x; L.cw[i][5] = v1.y; L.cw[i][6] = v1.z; L.cw[i][7] = v1.w;
+      } else if constexpr (BITS == 2) {
+        const uint2 v = *reinterpret_cast<const uint2*>(src);
+        L.cw[i][0] = v.x; L.cw[i][1] = v.y;
+      } else {
+        L.cw[i][0] = src[0]; L.cw[i][1] = src[1]; L.cw[i][2] = src[2];
+      }
+      L.s[i] = load_elem(a.scales, wn[i] * a.ngroups + g, a.sz_dtype);
+      L.z[i] = load_elem(a.zeros, wn[i] * a.ngroups + g, a.sz_dtype);
+    }
+    // B fragments: lane (r16, oct) holds X row 16 j + r16, columns 32 kk + 8 oct .. + 7
+    if constexpr (BM == 1) {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) L.x[kk][0] = loadx(b, kk, 0);
+    }
+  };
+
+  f32x4 acc[BN][BM];
+#pragma unroll
+  for (int i = 0; i < BN; ++i)
+#pragma unroll
+    for (int j = 0; j < BM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto block = [&](int b, const DsBlock<BITS, NT, MT>& L) {
+    // dequantise this lane's chunks into the wave's tile (row 16 i + r16, columns 32 oct ..)
+#pragma unroll
+    for (int i = 0; i < BN; ++i) {
+      uint32_t d[16];
+      dq_chunk<BITS, BF16>(L.cw[i], L.s[i], L.z[i], d, std::make_integer_sequence<int, 16>{});
+      uint4* dst = reinterpret_cast<uint4*>(tile + (16 * i + r16) * P + 32 * oct);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) dst[q] = uint4{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
+    }
+    wave_sync();
+    uint4 xs[2][BM];
+    if constexpr (BM > 1) {
+#pragma unroll
+      for (int j = 0; j < BM; ++j) xs[0][j] = loadx(b, 0, j);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      if constexpr (BM > 1) {
+        if (kk + 1 < 4) {
+#pragma unroll
+          for (int j = 0; j < BM; ++j) xs[(kk + 1) & 1][j] = loadx(b, kk + 1, j);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < BN; ++i) {
+        const uint4 fa = *reinterpret_cast<const uint4*>(tile + (16 * i + r16) * P + 32 * kk + 8 * oct);
+#pragma unroll
+        for (int j = 0; j < BM; ++j) {
+          const uint4 fb = BM == 1 ? L.x[kk & (DsBlock<BITS, NT, MT>::XB - 1)][0] : xs[kk & 1][j];
+          if constexpr (BF16)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, fa),
+                                                                __builtin_bit_cast(bf16x8, fb), acc[i][j], 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, fa),
+                                                               __builtin_bit_cast(f16x8, fb), acc[i][j], 0, 0, 0);
+        }
+      }
+    }
+    wave_sync();  // the tile is rewritten by the next block
+  };
+
+  // blocks b = wave, wave + WAVES, ...: two in flight
+  DsBlock<BITS, NT, MT> A, B;
+  int b = wave;
+  if (b < nblk) load(b, A);
+  for (;;) {
+    if (b >= nblk) break;
+    if (b + WAVES < nblk) load(b + WAVES, B);
+    block(b, A);
+    b += WAVES;
+    if (b >= nblk) break;
+    if (b + WAVES < nblk) load(b + WAVES, A);
+    block(b, B);
+    b += WAVES;
+  }
+
+  // sum the waves' tiles in wave order; 16x16 layout: lane l, register v ->
+  // W row 4 (l / 16) + v, X row l % 16
+  for (int w = 0; w < WAVES; ++w) {
+    if (wave == w) {
+#pragma unroll
+      for (int i = 0; i < BN; ++i)
+#pragma unroll
+        for (int j = 0; j < BM; ++j)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            float& r = red[(16 * j + r16) * NT + 16 * i + 4 * oct + v];
+            r = (w == 0 ? 0.0f : r) + acc[i][j][v];
+          }
+    }
+    __syncthreads();
+  }
+  for (int e = tid; e < NT * MT; e += 64 * WAVES) {
+    const int ml = e / NT, nl = e % NT;
+    const int64_t m = m0 + ml, n = n0 + nl;
+    if (m < a.M && n < a.N) {
+      float v = red[e];
+      if (a.bias) v += load_elem(a.bias, n, a.bias_dtype);
+      store_elem(a.y, m * a.N + n, a.y_dtype, v);
+    }
+  }
+}
+
+// Large products (M > 16 and at least 128 output tiles): one workgroup per
+// 128 x MT tile of (weight rows x activation rows), K in steps of 64.  Each
+// thread loads one 32-code chunk of one weight row per step, dequantises it
+// into a double-buffered LDS tile, and stages a piece of X beside it; the 4
+// waves (2 x 2) multiply 32x32x16 MFMA fragments from LDS.  The next step's
+// codes and X are in registers while the current step is multiplied.
+template <int MT>
+struct DtCfg {
+  static constexpr int NT = 128, KB = 64, CPR = KB / 32;
+  static constexpr int P = KB + 8;               // LDS row pitch (halves): 144 B, conflict-free fragment reads
+  static constexpr int XV = MT * KB / 8 / 256;   // 16-byte X pieces per thread and step
+};
+
+template <int BITS, bool BF16, int MT>
+__global__ __launch_bounds__(256) void dq_tile_k(LinArgs a) {
+  using C = DtCfg<MT>;
+  constexpr int NT = C::NT, KB = C::KB, P = C::P, XV = C::XV;
+  __shared__ __attribute__((aligned(16))) uint16_t sW[2][NT * P];
+  __shared__ __attribute__((aligned(16))) uint16_t sX[2][MT * P];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * NT;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * MT;
+  const int nsteps = static_cast<int>(a.K / KB);
+
+  const int wr = tid / C::CPR, wc = tid % C::CPR;
+  const int64_t wn = std::min<int64_t>(n0 + wr, a.N - 1);
+  const uint8_t* wrow = a.packed + wn * a.pitch;
+  uint32_t cw[BITS];
+  float cs = 0.0f, cz = 0.0f;
+  uint4 xr[XV];
+  auto load = [&](int step) {
+    const int64_t k = static_cast<int64_t>(step) * KB + 32 * wc;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(wrow + k * BITS / 8);
+    if constexpr (BITS == 4) {
+      const uint4 v = *reinterpret_cast<const uint4*>(src);
+      cw[0] = v.x; cw[1] = v.y; cw[2] = v.z; cw[3] = v.w;
+    } else if constexpr (BITS == 8) {
+      const uint4 v0 = reinterpret_cast<const uint4*>(src)[0], v1 = reinterpret_cast<const uint4*>(src)[1];
+      cw[0] = v0.x; cw[1] = v0.y; cw[2] = v0.z; cw[3] = v0.w; cw[4] = v1.x; cw[5] = v1.y; cw[6] = v1.z; cw[7] = v1.w;
+    } else if constexpr (BITS == 2) {
+      const uint2 v = *reinterpret_cast<const uint2*>(src);
+      cw[0] = v.x; cw[1] = v.y;
+    } else {
+      cw[0] = src[0]; cw[1] = src[1]; cw[2] = src[2];
+    }
+    const int64_t g = k / a.gs;
+    cs = load_elem(a.scales, wn * a.ngroups + g, a.sz_dtype);
+    cz = load_elem(a.zeros, wn * a.ngroups + g, a.sz_dtype);
+#pragma unroll
+    for (int v = 0; v < XV; ++v) {
+      const int e = tid + 256 * v;
+      const int64_t m = m0 + e / (KB / 8);
+      xr[v] = m < a.M ? *reinterpret_cast<const uint4*>(a.x + m * a.K + static_cast<int64_t>(step) * KB +
+                                                         8 * (e % (KB / 8)))
+                      : uint4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store = [&](int buf) {
+    uint32_t d[16];
+    dq_chunk<BITS, BF16>(cw, cs, cz, d, std::make_integer_sequence<int, 16>{});
+    uint4* dst = reinterpret_cast<uint4*>(&sW[buf][wr * P + 32 * wc]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dst[q] = uint4{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
+#pragma unroll
+    for (int v = 0; v < XV; ++v) {
+      const int e = tid + 256 * v;
+      *reinterpret_cast<uint4*>(&sX[buf][(e / (KB / 8)) * P + 8 * (e % (KB / 8))]) = xr[v];
+    }
+  };
+
+  // waves 2 x 2: 64 weight rows x MT / 2 activation rows each, 32 x 32 blocks
+  constexpr int BN = 2, BM = MT / 64;
+  const int wbase = 64 * (wave >> 1), mbase = (MT / 2) * (wave & 1);
+  f32x16 acc[BN][BM];
+#pragma unroll
+  for (int i = 0; i < BN; ++i)
+#pragma unroll
+    for (int j = 0; j < BM; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int kk = 0; kk < KB / 16; ++kk) {
+      uint4 fa[BN], fb[BM];
+#pragma unroll
+      for (int i = 0; i < BN; ++i)
+        fa[i] = *reinterpret_cast<const uint4*>(&sW[buf][(wbase + 32 * i + (lane & 31)) * P + 16 * kk + 8 * (lane >> 5)]);
+#pragma unroll
+      for (int j = 0; j < BM; ++j)
+        fb[j] = *reinterpret_cast<const uint4*>(&sX[buf][(mbase + 32 * j + (lane & 31)) * P + 16 * kk + 8 * (lane >> 5)]);
+#pragma unroll
+      for (int i = 0; i < BN; ++i)
+#pragma unroll
+        for (int j = 0; j < BM; ++j) {
+          if constexpr (BF16)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[i]),
+                                                                __builtin_bit_cast(bf16x8, fb[j]), acc[i][j], 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, fa[i]),
+                                                               __builtin_bit_cast(f16x8, fb[j]), acc[i][j], 0, 0, 0);
+        }
+    }
+  };
+
+  load(0);
+  store(0);
+  if (nsteps > 1) load(1);
+  __syncthreads();
+  for (int step = 0; step < nsteps; ++step) {
+    const int buf = step & 1;
+    compute(buf);
+    if (step + 1 < nsteps) {
+      store(buf ^ 1);
+      if (step + 2 < nsteps) load(step + 2);
+    }
+    __syncthreads();
+  }
+  // 32x32 layout: lane l, register v -> W row 8 (v / 4) + 4 (l / 32) + v % 4, X row l % 32
+#pragma unroll
+  for (int i = 0; i < BN; ++i)
+#pragma unroll
+    for (int j = 0; j < BM; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t n = n0 + wbase + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        const int64_t m = m0 + mbase + 32 * j + (lane & 31);
+        if (n < a.N && m < a.M) {
+          float r = acc[i][j][v];
+          if (a.bias) r += load_elem(a.bias, n, a.bias_dtype);
+          store_elem(a.y, m * a.N + n, a.y_dtype, r);
+        }
+      }
+}
+
+template <int BITS, bool BF16, int NT, int MT, int WAVES>
+int launch_split(hipStream_t st, const LinArgs& a) {
+  using C = DsCfg<NT, MT, WAVES>;
+  const dim3 grid(static_cast<unsigned>(cdiv(a.N, NT)), static_cast<unsigned>(cdiv(a.M, MT)));
+  hipLaunchKernelGGL((dq_split_k<BITS, BF16, NT, MT, WAVES>), grid, dim3(64 * WAVES), C::kLds, st, a);
+  return check_launch("dq_split");
+}
+
+// M <= 16: split-K with 16 waves, weight rows per workgroup chosen so that
+// the grid stays >= 256 workgroups while X is re-read by fewer of them;
+// M > 16: the tiled kernel when it has >= 128 tiles, else split-K
+template <int BITS, bool BF16>
+int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
+  if (a.M <= 16) {
+    if (a.N >= 64 * 256) return launch_split<BITS, BF16, 64, 16, 8>(st, a);
+    if (a.N >= 32 * 256) return launch_split<BITS, BF16, 32, 16, 16>(st, a);
+    return launch_split<BITS, BF16, 16, 16, 16>(st, a);
+  }
+  const int64_t mt = a.M <= 64 ? 64 : 128;
+  if (cdiv(a.N, 128) * cdiv(a.M, mt) >= 128) {
+    const dim3 grid(static_cast<unsigned>(cdiv(a.N, 128)), static_cast<unsigned>(cdiv(a.M, mt)));
+    if (mt == 64)
+      hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 64>), grid, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 128>), grid, dim3(256), 0, st, a);
+    return check_launch("dq_tile");
+  }
+  if (a.M <= 64) return launch_split<BITS, BF16, 32, 64, 8>(st, a);
+  return launch_split<BITS, BF16, 16, 128, 8>(st, a);
+}
+
 // ------------------------------------------------------------- generic ----
 __device__ __forceinline__ uint32_t code_at(const uint8_t* __restrict__ row, int64_t pitch, int64_t k, int bits) {
   if (bits == 0) return row[k];
@@ -809,6 +1223,8 @@ int launch_fast(hipStream_t st, const LinArgs& a) {
       return check_launch("gemv");
     }
   }
+  // 128-column blocks, one group per 32-code chunk
+  if (a.K % 128 == 0 && a.gs % 32 == 0) return launch_dq_gemm<BITS, BF16>(st, a);
   const dim3 grid(static_cast<unsigned>(cdiv(a.N, 16)), static_cast<unsigned>(cdiv(a.M, kMT * 16)));
   hipLaunchKernelGGL((dq_mfma_k<BITS, BF16>), grid, dim3(256), 0, st, a);
   return check_launch("dq_mfma");

@@ -224,3 +224,20 @@ def test_triton_quantized_linear(hip):
     # dequantized weights are close to the originals
     Wd = O.dequant(codes, s, z, np.arange(256) // 64)
     assert np.abs(Wd - w.numpy()).max() < 0.02 * 8 / 15 + 1e-3
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bits", [3, 4])
+@pytest.mark.parametrize("M,N,K,gs", [(16, 4101, 4096, 128), (9, 1000, 1024, 32), (64, 2050, 2048, 128),
+                                      (100, 1027, 4096, 64), (128, 4096, 4096, 128)])
+def test_linear_dequant_gemm(hip, xdt, bits, M, N, K, gs):
+    """M > 4: dequantise-then-MFMA kernel, ragged N and M, groups of 32-128
+    (one group per 32-code chunk), bias."""
+    from distributed_gptq_amd import _ops
+    codes, scales, zeros, x = _case(M, N, K, bits, gs, M + N + bits, xdt)
+    bias = torch.randn(N).to(xdt)
+    packed = torch.from_numpy(O.pack_bitstream(codes, bits)).cuda()
+    y = _ops.linear(x.cuda(), packed, bits, scales.cuda(), zeros.cuda(), K, group_size=gs, bias=bias.cuda())
+    ref = O.linear(x.float().numpy(), codes, scales.numpy(), zeros.numpy(), np.arange(K) // gs, bias.float().numpy())
+    err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err < TOL[xdt], err
