@@ -734,7 +734,7 @@ struct DsCfg {
   static constexpr int BN = NT / 16, BM = MT / 16;  // 16-row blocks of W and X
   static constexpr int CPL = NT / 16;               // 32-code chunks per lane and block
   static constexpr int P = 128 + 8;                 // LDS tile row pitch (halves)
-  static constexpr size_t kTile = static_cast<size_t>(NT) * P * 2;
+  static constexpr size_t kTile = static_cast<size_t>(16) * P * 2;  // one 16-row block at a time
   static constexpr size_t kLds = WAVES * kTile + static_cast<size_t>(NT) * MT * 4;
 };
 
@@ -815,8 +815,8 @@ __global__ __launch_bounds__(64 * WAVES) void dq_split_k(LinArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  uint16_t* tile = dsm + wave * (NT * P);
-  float* red = reinterpret_cast<float*>(dsm + WAVES * NT * P);
+  uint16_t* tile = dsm + wave * (16 * P);
+  float* red = reinterpret_cast<float*>(dsm + WAVES * 16 * P);
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * NT;
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * MT;
   const int nblk = static_cast<int>(a.K / 128);
@@ -880,32 +880,30 @@ __global__ __launch_bounds__(64 * WAVES) void dq_split_k(LinArgs a) {
     for (int j = 0; j < BM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   auto block = [&](int b, const DsBlock<BITS, NT, MT>& L) {
-    // dequantise this lane's chunks into the wave's tile (row 16 i + r16, columns 32 oct ..)
+    // row blocks one at a time through the wave's 16-row tile: dequantise this
+    // lane's chunk (row r16, columns 32 oct ..), then 4 MFMA steps against X
 #pragma unroll
     for (int i = 0; i < BN; ++i) {
       uint32_t d[16];
       dq_chunk<BITS, BF16>(L.cw[i], L.s[i], L.z[i], d, std::make_integer_sequence<int, 16>{});
-      uint4* dst = reinterpret_cast<uint4*>(tile + (16 * i + r16) * P + 32 * oct);
+      uint4* dst = reinterpret_cast<uint4*>(tile + r16 * P + 32 * oct);
 #pragma unroll
       for (int q = 0; q < 4; ++q) dst[q] = uint4{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
-    }
-    wave_sync();
-    uint4 xs[2][BM];
-    if constexpr (BM > 1) {
-#pragma unroll
-      for (int j = 0; j < BM; ++j) xs[0][j] = loadx(b, 0, j);
-    }
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
+      wave_sync();
+      uint4 xs[2][BM];
       if constexpr (BM > 1) {
-        if (kk + 1 < 4) {
 #pragma unroll
-          for (int j = 0; j < BM; ++j) xs[(kk + 1) & 1][j] = loadx(b, kk + 1, j);
-        }
+        for (int j = 0; j < BM; ++j) xs[0][j] = loadx(b, 0, j);
       }
 #pragma unroll
-      for (int i = 0; i < BN; ++i) {
-        const uint4 fa = *reinterpret_cast<const uint4*>(tile + (16 * i + r16) * P + 32 * kk + 8 * oct);
+      for (int kk = 0; kk < 4; ++kk) {
+        if constexpr (BM > 1) {
+          if (kk + 1 < 4) {
+#pragma unroll
+            for (int j = 0; j < BM; ++j) xs[(kk + 1) & 1][j] = loadx(b, kk + 1, j);
+          }
+        }
+        const uint4 fa = *reinterpret_cast<const uint4*>(tile + r16 * P + 32 * kk + 8 * oct);
 #pragma unroll
         for (int j = 0; j < BM; ++j) {
           const uint4 fb = BM == 1 ? L.x[kk & (DsBlock<BITS, NT, MT>::XB - 1)][0] : xs[kk & 1][j];
@@ -917,8 +915,8 @@ __global__ __launch_bounds__(64 * WAVES) void dq_split_k(LinArgs a) {
                                                                __builtin_bit_cast(f16x8, fb), acc[i][j], 0, 0, 0);
         }
       }
+      wave_sync();  // the tile is rewritten next
     }
-    wave_sync();  // the tile is rewritten by the next block
   };
 
   // blocks b = wave, wave + WAVES, ...: two in flight
