@@ -15,9 +15,15 @@
 //    of each row (a wave load covers 1 KiB of contiguous codes).  Within a
 //    chunk, codes are paired the way the packed word yields them cheaply
 //    ((0,4),(1,5).. for 4-bit), and x is stored in LDS in that order.
-//  * dq_mfma_k (larger M): v_mfma_f32_16x16x32_{f16,bf16} on 16 weight rows x
-//    16 activation rows per step, 4 waves splitting K; partial sums reduced in
-//    LDS.
+//  * dq_split_k / dq_tile_k (M > 4, K % 128 == 0, group size % 32 == 0):
+//    codes are dequantised to the activation type ((q - z) exact, one
+//    rounding of the product with s; for fp16 with integer zeros in [0, 1023]
+//    a packed magic-exponent form), written to LDS and fed to
+//    v_mfma_f32_16x16x32_{f16,bf16} (dq_split_k: the waves of a workgroup
+//    split K over 128-column blocks and reduce through LDS; dq_tile_k:
+//    128-row weight tiles x 64/128 activation rows, double-buffered LDS).
+//  * dq_mfma_k (other M > 4 layouts): 16 weight rows x 16 activation rows per
+//    MFMA step with zero points folded per group, 4 waves splitting K.
 //  * linear_generic: any layout (fp32 x, g_idx, ragged K): one wave per
 //    output, fp32.
 #include "common.hpp"
