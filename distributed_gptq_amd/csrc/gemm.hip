@@ -7,8 +7,11 @@
 // current one is multiplied.  Tiles are 128 x 64 (64 x 64 for products that
 // would give fewer than 256 such tiles), 32 deep: small tiles keep enough
 // waves resident per CU to hide the load latency of this single-buffered
-// pipeline, which measured faster than 128 x 128 or 256 x 128 tiles for
-// every product of the factorisation and the sweep.  Triangular operands
+// pipeline, which measured faster than 128 x 128 or 256 x 128 tiles, and
+// than a double-buffered variant with one barrier per stage (fewer resident
+// waves), for every product of the factorisation and the sweep.  Operand
+// transposition is a compile-time parameter and the loads are branch-free
+// (see load_op).  Triangular operands
 // skip the k-tiles that are known to be zero; GEMM_C_LOWER skips tiles
 // strictly above the diagonal.
 #include "gemm.hpp"
@@ -26,54 +29,49 @@ struct Operand {
 };
 
 // Loads the stage (r0..r0+TR-1, k0..k0+BK-1) of an operand viewed as [r][k]
-// into registers: TR * BK / 4 float4, NQ per thread.
-template <int TR, int BK, bool kVec>
+// into registers: TR * BK / 4 float4, NQ per thread.  Elements outside the
+// operand read as zero.  Branch-free: an out-of-range lane loads from the
+// operand's first element and selects zero, so the loads of a stage stay in
+// flight together (a divergent branch around each load made the compiler
+// wait for every load before the next one).  kVec: every float4 is entirely
+// inside or entirely outside the operand (16-byte aligned rows and a
+// contiguous extent that is a multiple of 4).
+template <int TR, int BK, bool kVec, bool kTrans>
 __device__ __forceinline__ void load_op(const Operand& o, int64_t r0, int64_t k0, int64_t Kd, int tid,
                                         f32x4 (&pre)[TR * BK / 4 / kThreads]) {
   constexpr int NQ = TR * BK / 4 / kThreads;
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     const int idx = q * kThreads + tid;
-    f32x4 v = {0.f, 0.f, 0.f, 0.f};
-    if (!o.trans) {
-      // contiguous along k: BK / 4 lanes per row
-      const int64_t r = r0 + idx / (BK / 4);
-      const int64_t k = k0 + (idx % (BK / 4)) * 4;
-      if (r < o.rows) {
-        const float* src = o.p + r * o.ld + k;
-        if (kVec && k + 3 < Kd) {
-          v = *reinterpret_cast<const f32x4*>(src);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = (k + e < Kd) ? src[e] : 0.0f;
-        }
-      }
+    // contiguous along k (BK / 4 lanes per row), or along r when transposed (TR / 4 lanes per k-row)
+    const int64_t r = kTrans ? r0 + (idx % (TR / 4)) * 4 : r0 + idx / (BK / 4);
+    const int64_t k = kTrans ? k0 + idx / (TR / 4) : k0 + (idx % (BK / 4)) * 4;
+    const int64_t off = kTrans ? k * o.ld + r : r * o.ld + k;
+    f32x4 v;
+    if constexpr (kVec) {
+      const bool ok = r < o.rows && k < Kd;
+      v = *reinterpret_cast<const f32x4*>(o.p + (ok ? off : 0));
+      if (!ok) v = f32x4{0.f, 0.f, 0.f, 0.f};
     } else {
-      // contiguous along r: TR / 4 lanes per k-row
-      const int64_t k = k0 + idx / (TR / 4);
-      const int64_t r = r0 + (idx % (TR / 4)) * 4;
-      if (k < Kd) {
-        const float* src = o.p + k * o.ld + r;
-        if (kVec && r + 3 < o.rows) {
-          v = *reinterpret_cast<const f32x4*>(src);
-        } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = (r + e < o.rows) ? src[e] : 0.0f;
-        }
+      for (int e = 0; e < 4; ++e) {
+        const bool ok = kTrans ? (r + e < o.rows && k < Kd) : (r < o.rows && k + e < Kd);
+        const float x = o.p[ok ? off + e : 0];
+        v[e] = ok ? x : 0.0f;
       }
     }
     pre[q] = v;
   }
 }
 
-template <int TR, int BK>
-__device__ __forceinline__ void store_op(bool trans, float* s, int tid, const f32x4 (&pre)[TR * BK / 4 / kThreads]) {
+template <int TR, int BK, bool trans>
+__device__ __forceinline__ void store_op(float* s, int tid, const f32x4 (&pre)[TR * BK / 4 / kThreads]) {
   constexpr int NQ = TR * BK / 4 / kThreads;
   constexpr int P = BK + 2;
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     const int idx = q * kThreads + tid;
-    if (!trans) {
+    if constexpr (!trans) {
       const int r = idx / (BK / 4), k = (idx % (BK / 4)) * 4;
       float2* d = reinterpret_cast<float2*>(s + r * P + k);
       d[0] = make_float2(pre[q][0], pre[q][1]);
@@ -86,7 +84,7 @@ __device__ __forceinline__ void store_op(bool trans, float* s, int tid, const f3
   }
 }
 
-template <int TM, int TN, int BK, bool kVec>
+template <int TM, int TN, int BK, bool kVec, bool kTA, bool kTB>
 __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(int64_t M, int64_t N, int64_t Kd, float alpha,
                                                            Operand a, Operand b, float beta, float* __restrict__ C,
                                                            int64_t ldc, int flags, int tiles_n) {
@@ -124,17 +122,17 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(int64_t M, int64_t N
 
   f32x4 pa[QA], pb[QB];
   if (kb < ke) {
-    load_op<TM, BK, kVec>(a, i0, kb, Kd, tid, pa);
-    load_op<TN, BK, kVec>(b, j0, kb, Kd, tid, pb);
+    load_op<TM, BK, kVec, kTA>(a, i0, kb, Kd, tid, pa);
+    load_op<TN, BK, kVec, kTB>(b, j0, kb, Kd, tid, pb);
   }
   for (int64_t k0 = kb; k0 < ke; k0 += BK) {
     __syncthreads();
-    store_op<TM, BK>(a.trans, sA, tid, pa);
-    store_op<TN, BK>(b.trans, sB, tid, pb);
+    store_op<TM, BK, kTA>(sA, tid, pa);
+    store_op<TN, BK, kTB>(sB, tid, pb);
     __syncthreads();
     if (k0 + BK < ke) {
-      load_op<TM, BK, kVec>(a, i0, k0 + BK, Kd, tid, pa);
-      load_op<TN, BK, kVec>(b, j0, k0 + BK, Kd, tid, pb);
+      load_op<TM, BK, kVec, kTA>(a, i0, k0 + BK, Kd, tid, pa);
+      load_op<TN, BK, kVec, kTB>(b, j0, k0 + BK, Kd, tid, pb);
     }
 #pragma unroll
     for (int kk = 0; kk < BK / 2; ++kk) {
@@ -184,19 +182,43 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(int64_t M, int64_t N
     }
 }
 
-template <int TM, int TN, int BK>
-int launch_tiles(hipStream_t st, int64_t M, int64_t N, int64_t Kd, float alpha, const Operand& a, const Operand& b,
-                 bool vec, float beta, float* C, int64_t ldc, int flags) {
-  const int tiles_m = static_cast<int>(cdiv(M, TM));
-  const int tiles_n = static_cast<int>(cdiv(N, TN));
-  const dim3 grid(static_cast<unsigned>(tiles_m) * tiles_n);
-  if (vec)
-    hipLaunchKernelGGL((gemm_f32_kernel<TM, TN, BK, true>), grid, dim3(kThreads), 0, st, M, N, Kd, alpha, a, b, beta,
-                       C, ldc, flags, tiles_n);
-  else
-    hipLaunchKernelGGL((gemm_f32_kernel<TM, TN, BK, false>), grid, dim3(kThreads), 0, st, M, N, Kd, alpha, a, b,
-                       beta, C, ldc, flags, tiles_n);
+struct GemmArgs {
+  int64_t M, N, Kd;
+  float alpha;
+  Operand a, b;
+  float beta;
+  float* C;
+  int64_t ldc;
+  int flags;
+};
+
+template <int TM, int TN, bool V, bool TA, bool TB>
+void launch_one(hipStream_t st, const GemmArgs& g) {
+  const int tiles_n = static_cast<int>(cdiv(g.N, TN));
+  const dim3 grid(static_cast<unsigned>(cdiv(g.M, TM) * tiles_n));
+  hipLaunchKernelGGL((gemm_f32_kernel<TM, TN, 32, V, TA, TB>), grid, dim3(kThreads), 0, st, g.M, g.N, g.Kd, g.alpha,
+                     g.a, g.b, g.beta, g.C, g.ldc, g.flags, tiles_n);
+}
+
+// transposition and vector width are compile-time in the kernel
+template <int TM, int TN, bool V>
+void launch_trans(hipStream_t st, const GemmArgs& g) {
+  if (!g.a.trans && !g.b.trans) launch_one<TM, TN, V, false, false>(st, g);
+  else if (!g.a.trans) launch_one<TM, TN, V, false, true>(st, g);
+  else if (!g.b.trans) launch_one<TM, TN, V, true, false>(st, g);
+  else launch_one<TM, TN, V, true, true>(st, g);
+}
+
+template <int TM, int TN>
+int launch_tiles(hipStream_t st, const GemmArgs& g, bool vec) {
+  if (vec) launch_trans<TM, TN, true>(st, g);
+  else launch_trans<TM, TN, false>(st, g);
   return check_launch("gemm_f32");
+}
+
+// every float4 of the operand is entirely inside or outside it
+inline bool vec_ok(const Operand& o, int64_t Kd) {
+  return o.ld % 4 == 0 && (reinterpret_cast<uintptr_t>(o.p) % 16) == 0 && (o.trans ? o.rows : Kd) % 4 == 0;
 }
 
 }  // namespace
@@ -205,13 +227,11 @@ int launch_gemm_f32(hipStream_t st, int64_t M, int64_t N, int64_t Kd, float alph
                     bool transA, const float* B, int64_t ldb, bool transB, float beta, float* C, int64_t ldc,
                     int flags) {
   if (M <= 0 || N <= 0) return GPTQ_OK;
-  Operand a{A, lda, transA, M};
-  Operand b{B, ldb, !transB, N};  // operand B is viewed as [j][k]: B^T
-  const bool vec = lda % 4 == 0 && ldb % 4 == 0 && (reinterpret_cast<uintptr_t>(A) % 16) == 0 &&
-                   (reinterpret_cast<uintptr_t>(B) % 16) == 0;
-  if (cdiv(M, 128) * cdiv(N, 64) < 256)
-    return launch_tiles<64, 64, 32>(st, M, N, Kd, alpha, a, b, vec, beta, C, ldc, flags);
-  return launch_tiles<128, 64, 32>(st, M, N, Kd, alpha, a, b, vec, beta, C, ldc, flags);
+  const GemmArgs g{M, N, Kd, alpha, Operand{A, lda, transA, M}, Operand{B, ldb, !transB, N},  // B viewed as [j][k]
+                   beta, C, ldc, flags};
+  const bool vec = vec_ok(g.a, Kd) && vec_ok(g.b, Kd);
+  if (cdiv(M, 128) * cdiv(N, 64) < 256) return launch_tiles<64, 64>(st, g, vec);
+  return launch_tiles<128, 64>(st, g, vec);
 }
 
 }  // namespace gptq
