@@ -210,13 +210,22 @@ __global__ __launch_bounds__(256) void chol_inv_leaf(float* __restrict__ A, floa
   // load the lower triangle (identity padding beyond m), 32 loads in flight per thread
   for (int e0 = tid; e0 < kNB * kNB; e0 += 256 * 32) {
     float v[32];
+    // unconditional loads (clamped into the block), selected afterwards; the
+    // scheduling barrier keeps every select after the last load (placed next
+    // to its load, each select made the wave wait for that load before
+    // issuing the next)
 #pragma unroll
     for (int u = 0; u < 32; ++u) {
-      // unconditional loads (clamped into the block), selected afterwards
       const int e = e0 + u * 256;
       const int rr = e >> 7, cc = e & (kNB - 1);
-      const float t = A[(n0 + min(rr, m - 1)) * ld + n0 + min(cc, m - 1)];
-      v[u] = (rr < m && cc < m && cc <= rr) ? t : (rr == cc ? 1.0f : 0.0f);
+      v[u] = A[(n0 + min(rr, m - 1)) * ld + n0 + min(cc, m - 1)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 32; ++u) {
+      const int e = e0 + u * 256;
+      const int rr = e >> 7, cc = e & (kNB - 1);
+      v[u] = (rr < m && cc < m && cc <= rr) ? v[u] : (rr == cc ? 1.0f : 0.0f);
     }
 #pragma unroll
     for (int u = 0; u < 32; ++u) {

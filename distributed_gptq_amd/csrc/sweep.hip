@@ -220,23 +220,31 @@ __global__ __launch_bounds__(64 * kSW) void sweep_r16(SubArgs a) {
   const int n = a.n;
   constexpr int kThr = 64 * kSW;
 
-  // Stage T (16 vector loads per thread in flight before any is stored).
+  // Stage T: 16 vector loads per thread in flight before any is stored.  The
+  // loads are branch-free (an element outside the block loads the block's
+  // first element and is replaced by zero): loads under divergent branches
+  // were each waited for before the next one was issued.
   const float* tsrc = a.T + a.j1 * a.ldt + a.j1;
   const bool tvec = (n & 3) == 0 && (a.ldt & 3) == 0 && (reinterpret_cast<uintptr_t>(tsrc) & 15) == 0;
   {
     f32x4 v[16];
+    if (tvec) {
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int e = tid + u * kThr, j = e >> 5, c = 4 * (e & 31);
-      v[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      if (j < n) {
-        const float* src = tsrc + j * a.ldt + c;
-        if (tvec) {
-          if (c < n) v[u] = *reinterpret_cast<const f32x4*>(src);
-        } else {
+      for (int u = 0; u < 16; ++u) {
+        const int e = tid + u * kThr, j = e >> 5, c = 4 * (e & 31);
+        const bool ok = j < n && c < n;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(tsrc + (ok ? j * a.ldt + c : 0));
+        v[u] = ok ? x : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+    } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (c + i < n) v[u][i] = src[i];
+      for (int u = 0; u < 16; ++u) {
+        const int e = tid + u * kThr, j = e >> 5, c = 4 * (e & 31);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bool ok = j < n && c + i < n;
+          const float x = tsrc[ok ? j * a.ldt + c + i : 0];
+          v[u][i] = ok ? x : 0.0f;
         }
       }
     }
@@ -251,17 +259,24 @@ __global__ __launch_bounds__(64 * kSW) void sweep_r16(SubArgs a) {
   {
     const float* src = a.W + rrow * a.cols + a.j1;
     const bool wvec = (n & 3) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0;
+    if (wvec) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int c = 64 * h + 4 * q;
-      if (wvec) {
-        const f32x4 v = c < n ? *reinterpret_cast<const f32x4*>(src + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int h = 0; h < 2; ++h) {
+        const int c = 64 * h + 4 * q;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(src + (c < n ? c : 0));
+        const f32x4 v = c < n ? x : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int u = 0; u < 4; ++u) st.w[4 * h + u] = v[u];
-      } else {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) st.w[4 * h + u] = c + u < n ? src[c + u] : 0.0f;
       }
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int c = 64 * h + 4 * q + u;
+          const float x = src[c < n ? c : 0];
+          st.w[4 * h + u] = c < n ? x : 0.0f;
+        }
     }
   }
   __syncthreads();
@@ -273,13 +288,12 @@ __global__ __launch_bounds__(64 * kSW) void sweep_r16(SubArgs a) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int c = q + 16 * u;
-      f32x4 r = f32x4{1.0f, 0.0f, 1.0f, 1.0f};
-      if (c < n) {
-        const int g = a.gs > 0 ? (c0 + c) / a.gs : 0;
-        const float sg = a.scale[rrow * a.ngroups + a.g_lo + g];
-        r = f32x4{sg, a.zero[rrow * a.ngroups + a.g_lo + g], 1.0f / sg, 1.0f / Tl[c * 128 + c]};
-      }
-      pcol[c * kSRows + rl] = r;
+      const int cc = c < n ? c : 0;  // branch-free loads, as for T
+      const int g = a.gs > 0 ? (c0 + cc) / a.gs : 0;
+      const float sg = a.scale[rrow * a.ngroups + a.g_lo + g];
+      const float zg = a.zero[rrow * a.ngroups + a.g_lo + g];
+      const f32x4 r = f32x4{sg, zg, 1.0f / sg, 1.0f / Tl[c * 128 + c]};
+      pcol[c * kSRows + rl] = c < n ? r : f32x4{1.0f, 0.0f, 1.0f, 1.0f};
     }
   }
 #pragma unroll
