@@ -967,6 +967,163 @@ __global__ __launch_bounds__(64 * WAVES) void dq_split_k(LinArgs a) {
   }
 }
 
+// M <= 16, fp16 activations, 4-bit codes: the dequantised codes go straight
+// from registers into the MFMA, with no LDS tile.  Lane (r, g) of a wave loads
+// codes 32 g .. 32 g + 31 of the 128-column block for weight row r (one
+// 16-byte load); at MFMA step kk it supplies the 8 codes of word kk, so step
+// kk covers columns {32 g + 8 kk + t} over the four lane groups g -- a fixed
+// bijection of the block's columns onto (step, lane group, element), which
+// the X fragments follow (lane (m, g) at step kk holds X row m at the same 8
+// columns).  Within a word the codes are decoded as pairs (t, t + 4) (an
+// AND-OR against a 1024 exponent per pair), so both operands carry their 8
+// elements in the order 0 4 1 5 2 6 3 7 (X is permuted with v_perm).  The
+// dequantised value is (q - z) (exact) times s, rounded once, as in the LDS
+// path.  The waves of a workgroup split the blocks and sum their partial
+// tiles in wave order.
+template <int NT>
+struct DrBlock {
+  uint4 cw[NT / 16];
+  uint4 x[4];
+};
+
+__device__ __forceinline__ uint4 perm_0415(uint4 v) {
+  return uint4{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+               __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
+}
+
+// word w (codes t = 0..7 at bits 4t) -> 4 dwords: (code t, code t + 4) for t = 0..3
+template <bool kPacked>
+__device__ __forceinline__ uint4 dq_word_0415(uint32_t w, uint32_t zz, uint32_t sh, float s, float z) {
+  uint32_t p[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) p[t] = (w >> (4 * t)) & 0x000F000Fu;
+  if constexpr (kPacked) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) p[t] = dq_pair16(p[t], zz, sh);
+  } else {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) p[t] = dq_pair<false>(p[t], s, z);
+  }
+  return uint4{p[0], p[1], p[2], p[3]};
+}
+
+template <int NT, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
+  constexpr int BN = NT / 16;
+  __shared__ float red[WAVES][BN][4][64];
+  extern __shared__ float2 sz[];  // [NT][ngroups]: (scale, zero) of the workgroup's rows
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * NT;
+  const int nblk = static_cast<int>(a.K / 128);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int ng = static_cast<int>(a.ngroups);
+
+  // the workgroup's scales and zeros (contiguous rows of the [N][ngroups]
+  // arrays) are staged once with coalesced loads: per block a lane then reads
+  // its pair from LDS instead of two 16-row gathers
+  for (int e = tid; e < NT * ng; e += 64 * WAVES) {
+    const int64_t n = std::min<int64_t>(n0 + e / ng, a.N - 1);
+    const int64_t off = n * a.ngroups + e % ng;
+    sz[e] = float2{load_elem(a.scales, off, a.sz_dtype), load_elem(a.zeros, off, a.sz_dtype)};
+  }
+  __syncthreads();
+
+  const uint8_t* wrow[BN];
+  int64_t wn[BN];
+#pragma unroll
+  for (int i = 0; i < BN; ++i) {
+    wn[i] = std::min<int64_t>(n0 + 16 * i + r16, a.N - 1);
+    wrow[i] = a.packed + wn[i] * a.pitch;
+  }
+  const bool xok = r16 < a.M;
+  const uint16_t* xrow = a.x + (xok ? r16 : 0) * a.K;
+
+  auto load = [&](int b, DrBlock<NT>& L) {
+    const int64_t k = static_cast<int64_t>(b) * 128 + 32 * g4;
+#pragma unroll
+    for (int i = 0; i < BN; ++i) L.cw[i] = *reinterpret_cast<const uint4*>(wrow[i] + k / 2);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) L.x[kk] = *reinterpret_cast<const uint4*>(xrow + k + 8 * kk);
+  };
+
+  f32x4 acc[BN];
+#pragma unroll
+  for (int i = 0; i < BN; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto block = [&](int b, const DrBlock<NT>& L) {
+    uint4 xb[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) xb[kk] = xok ? perm_0415(L.x[kk]) : uint4{0u, 0u, 0u, 0u};
+    const int g = static_cast<int>((static_cast<int64_t>(b) * 128 + 32 * g4) / a.gs);
+#pragma unroll
+    for (int i = 0; i < BN; ++i) {
+      const float2 p = sz[(16 * i + r16) * ng + g];
+      const float s = p.x, z = p.y;
+      const uint32_t w[4] = {L.cw[i].x, L.cw[i].y, L.cw[i].z, L.cw[i].w};
+      uint4 fa[4];
+      // GPTQ zero points are integers: the packed path, chosen for the whole wave
+      if (__all(z == rintf(z) && z >= 0.0f && z <= 1023.0f)) {
+        const uint32_t zz = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(1024.0f + z),
+                                                                static_cast<_Float16>(1024.0f + z)});
+        const uint32_t sh = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(s), static_cast<_Float16>(s)});
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) fa[kk] = dq_word_0415<true>(w[kk], zz, sh, s, z);
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) fa[kk] = dq_word_0415<false>(w[kk], 0u, 0u, s, z);
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, fa[kk]),
+                                                        __builtin_bit_cast(f16x8, xb[kk]), acc[i], 0, 0, 0);
+    }
+  };
+
+  // blocks b = wave, wave + WAVES, ...: two in flight
+  DrBlock<NT> A, B;
+  int b = wave;
+  if (b < nblk) load(b, A);
+  for (;;) {
+    if (b >= nblk) break;
+    if (b + WAVES < nblk) load(b + WAVES, B);
+    block(b, A);
+    b += WAVES;
+    if (b >= nblk) break;
+    if (b + WAVES < nblk) load(b + WAVES, A);
+    block(b, B);
+    b += WAVES;
+  }
+
+  // partial tiles summed in wave order; 16x16 layout: lane l, register v ->
+  // W row 4 (l / 16) + v, X row l % 16
+#pragma unroll
+  for (int i = 0; i < BN; ++i)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) red[wave][i][v][lane] = acc[i][v];
+  __syncthreads();
+  for (int e = tid; e < BN * 4 * 64; e += 64 * WAVES) {
+    const int i = e / 256, v = (e / 64) % 4, l = e % 64;
+    float r = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) r += red[w][i][v][l];
+    const int64_t m = l % 16, n = n0 + 16 * i + 4 * (l / 16) + v;
+    if (m < a.M && n < a.N) {
+      if (a.bias) r += load_elem(a.bias, n, a.bias_dtype);
+      store_elem(a.y, m * a.N + n, a.y_dtype, r);
+    }
+  }
+}
+
+template <int NT, int WAVES>
+int launch_reg4(hipStream_t st, const LinArgs& a) {
+  const size_t lds = static_cast<size_t>(NT) * a.ngroups * sizeof(float2);
+  hipLaunchKernelGGL((dq_reg4_k<NT, WAVES>), dim3(static_cast<unsigned>(cdiv(a.N, NT))), dim3(64 * WAVES), lds, st,
+                     a);
+  return check_launch("dq_reg4");
+}
+
 // Large products (M > 16 and at least 128 output tiles): one workgroup per
 // 128 x MT tile of (weight rows x activation rows), K in steps of 64.  Each
 // thread loads one 32-code chunk of one weight row per step, dequantises it
@@ -1116,6 +1273,14 @@ int launch_split(hipStream_t st, const LinArgs& a) {
 // M > 16: the tiled kernel when it has >= 128 tiles, else split-K
 template <int BITS, bool BF16>
 int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
+  if constexpr (BITS == 4 && !BF16) {
+    // the register path stages the workgroup's scales and zeros in <= 64 KB of LDS
+    if (a.M <= 16 && 64 * a.ngroups * sizeof(float2) <= 64 * 1024) {
+      if (a.N >= 64 * 256) return launch_reg4<64, 8>(st, a);
+      if (a.N >= 32 * 256) return launch_reg4<32, 8>(st, a);
+      return launch_reg4<16, 16>(st, a);
+    }
+  }
   if (a.M <= 16) {
     if (a.N >= 64 * 256) return launch_split<BITS, BF16, 64, 16, 8>(st, a);
     if (a.N >= 32 * 256) return launch_split<BITS, BF16, 32, 16, 16>(st, a);
