@@ -1007,7 +1007,14 @@ __device__ __forceinline__ uint4 dq_word_0415(uint32_t w, uint32_t zz, uint32_t 
   return uint4{p[0], p[1], p[2], p[3]};
 }
 
-template <int NT, int WAVES>
+// kFold (group size a multiple of 128, so a block is one group): the codes
+// enter the MFMA as the small integers q (exact in fp16, products exact in
+// fp32), and each block's 16 x 16 result is corrected per weight row as
+// s (sum q x - z sum x), with sum x from one more MFMA chain against an
+// all-ones operand.  This is the per-group zero folding of the reference's
+// fused kernels; it skips the per-weight subtract, multiply and fp16
+// rounding of the dequantised weight.
+template <int NT, int WAVES, bool kFold>
 __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
   constexpr int BN = NT / 16;
   __shared__ float red[WAVES][BN][4][64];
@@ -1057,6 +1064,36 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) xb[kk] = xok ? perm_0415(L.x[kk]) : uint4{0u, 0u, 0u, 0u};
     const int g = static_cast<int>((static_cast<int64_t>(b) * 128 + 32 * g4) / a.gs);
+    if constexpr (kFold) {
+      f32x4 sx = f32x4{0.f, 0.f, 0.f, 0.f};
+      const uint4 ones = uint4{0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        sx = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ones), __builtin_bit_cast(f16x8, xb[kk]),
+                                                    sx, 0, 0, 0);
+      const f16x2 magic = __builtin_bit_cast(f16x2, 0x64006400u);
+#pragma unroll
+      for (int i = 0; i < BN; ++i) {
+        const uint32_t w[4] = {L.cw[i].x, L.cw[i].y, L.cw[i].z, L.cw[i].w};
+        f32x4 t = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          uint32_t q[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            q[u] = __builtin_bit_cast(uint32_t,
+                                      __builtin_bit_cast(f16x2, ((w[kk] >> (4 * u)) & 0x000F000Fu) | 0x64006400u) - magic);
+          t = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, uint4{q[0], q[1], q[2], q[3]}),
+                                                     __builtin_bit_cast(f16x8, xb[kk]), t, 0, 0, 0);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float2 p = sz[(16 * i + 4 * g4 + v) * ng + g];
+          acc[i][v] = fmaf(p.x, fmaf(-p.y, sx[v], t[v]), acc[i][v]);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < BN; ++i) {
       const float2 p = sz[(16 * i + r16) * ng + g];
@@ -1119,8 +1156,11 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
 template <int NT, int WAVES>
 int launch_reg4(hipStream_t st, const LinArgs& a) {
   const size_t lds = static_cast<size_t>(NT) * a.ngroups * sizeof(float2);
-  hipLaunchKernelGGL((dq_reg4_k<NT, WAVES>), dim3(static_cast<unsigned>(cdiv(a.N, NT))), dim3(64 * WAVES), lds, st,
-                     a);
+  const dim3 grid(static_cast<unsigned>(cdiv(a.N, NT)));
+  if (a.gs % 128 == 0)
+    hipLaunchKernelGGL((dq_reg4_k<NT, WAVES, true>), grid, dim3(64 * WAVES), lds, st, a);
+  else
+    hipLaunchKernelGGL((dq_reg4_k<NT, WAVES, false>), grid, dim3(64 * WAVES), lds, st, a);
   return check_launch("dq_reg4");
 }
 
