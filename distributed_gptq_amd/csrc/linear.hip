@@ -1027,15 +1027,6 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
   const int r16 = lane & 15, g4 = lane >> 4;
   const int ng = static_cast<int>(a.ngroups);
 
-  // the workgroup's scales and zeros (contiguous rows of the [N][ngroups]
-  // arrays) are staged once with coalesced loads: per block a lane then reads
-  // its pair from LDS instead of two 16-row gathers
-  for (int e = tid; e < NT * ng; e += 64 * WAVES) {
-    const int64_t n = std::min<int64_t>(n0 + e / ng, a.N - 1);
-    const int64_t off = n * a.ngroups + e % ng;
-    sz[e] = float2{load_elem(a.scales, off, a.sz_dtype), load_elem(a.zeros, off, a.sz_dtype)};
-  }
-  __syncthreads();
 
   const uint8_t* wrow[BN];
   int64_t wn[BN];
@@ -1118,13 +1109,26 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
     }
   };
 
-  // blocks b = wave, wave + WAVES, ...: two in flight
+  // blocks b = wave, wave + WAVES, ...: two in flight; the first two are
+  // issued before the scales and zeros are staged
   DrBlock<NT> A, B;
   int b = wave;
   if (b < nblk) load(b, A);
-  for (;;) {
+  if (b + WAVES < nblk) load(b + WAVES, B);
+
+  // the workgroup's scales and zeros (contiguous rows of the [N][ngroups]
+  // arrays) are staged once with coalesced loads: per block a lane then reads
+  // its pairs from LDS instead of 16-row gathers
+  for (int e = tid; e < NT * ng; e += 64 * WAVES) {
+    const int64_t n = std::min<int64_t>(n0 + e / ng, a.N - 1);
+    const int64_t off = n * a.ngroups + e % ng;
+    sz[e] = float2{load_elem(a.scales, off, a.sz_dtype), load_elem(a.zeros, off, a.sz_dtype)};
+  }
+  __syncthreads();
+
+  for (bool first = true;; first = false) {
     if (b >= nblk) break;
-    if (b + WAVES < nblk) load(b + WAVES, B);
+    if (!first && b + WAVES < nblk) load(b + WAVES, B);
     block(b, A);
     b += WAVES;
     if (b >= nblk) break;
