@@ -1160,6 +1160,9 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
 template <int NT, int WAVES>
 int launch_reg4(hipStream_t st, const LinArgs& a) {
   const size_t lds = static_cast<size_t>(NT) * a.ngroups * sizeof(float2);
+  // static partial-tile buffer + the staged scales and zeros within the CU's LDS
+  GPTQ_REQUIRE(static_cast<size_t>(WAVES) * NT * 16 * sizeof(float) + lds <= 160 * 1024, GPTQ_ERR_SHAPE,
+               "dq_reg4: %lld groups per row exceed the LDS budget", static_cast<long long>(a.ngroups));
   const dim3 grid(static_cast<unsigned>(cdiv(a.N, NT)));
   if (a.gs % 128 == 0)
     hipLaunchKernelGGL((dq_reg4_k<NT, WAVES, true>), grid, dim3(64 * WAVES), lds, st, a);
@@ -1320,9 +1323,10 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
   if constexpr (BITS == 4 && !BF16) {
     // the register path stages the workgroup's scales and zeros in <= 64 KB of LDS
     if (a.M <= 16 && 64 * a.ngroups * sizeof(float2) <= 64 * 1024) {
-      if (a.N >= 64 * 256) return launch_reg4<64, 8>(st, a);
-      if (a.N >= 32 * 256) return launch_reg4<32, 8>(st, a);
-      return launch_reg4<16, 16>(st, a);
+      // measured best per shape class (28672 x 4096, 14336 x 4096, 4096 x 14336)
+      if (a.N >= 64 * 256) return launch_reg4<64, 4>(st, a);
+      if (a.N >= 32 * 256) return launch_reg4<64, 8>(st, a);
+      return launch_reg4<16, 8>(st, a);
     }
   }
   if (a.M <= 16) {
