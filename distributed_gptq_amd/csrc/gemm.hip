@@ -30,16 +30,19 @@ struct Operand {
 
 // Loads the stage (r0..r0+TR-1, k0..k0+BK-1) of an operand viewed as [r][k]
 // into registers: TR * BK / 4 float4, NQ per thread.  Elements outside the
-// operand read as zero.  Branch-free: an out-of-range lane loads from the
-// operand's first element and selects zero, so the loads of a stage stay in
-// flight together (a divergent branch around each load made the compiler
-// wait for every load before the next one).  kVec: every float4 is entirely
-// inside or entirely outside the operand (16-byte aligned rows and a
-// contiguous extent that is a multiple of 4).
+// operand are flagged in `ok` (bit 4 q + e) and zeroed by store_op.  Branch-
+// free: an out-of-range lane loads from the operand's first element.  Both
+// choices keep the loads in flight across the stage's MFMAs: a divergent
+// branch around each load, or a select right after it, made the compiler wait
+// for the loads before the multiply.  kVec: every float4 is entirely inside
+// or entirely outside the operand (16-byte aligned rows and a contiguous
+// extent that is a multiple of 4).
 template <int TR, int BK, bool kVec, bool kTrans>
 __device__ __forceinline__ void load_op(const Operand& o, int64_t r0, int64_t k0, int64_t Kd, int tid,
-                                        f32x4 (&pre)[TR * BK / 4 / kThreads]) {
+                                        f32x4 (&pre)[TR * BK / 4 / kThreads], uint32_t& ok) {
   constexpr int NQ = TR * BK / 4 / kThreads;
+  static_assert(NQ <= 8, "validity bits");
+  ok = 0;
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     const int idx = q * kThreads + tid;
@@ -47,27 +50,29 @@ __device__ __forceinline__ void load_op(const Operand& o, int64_t r0, int64_t k0
     const int64_t r = kTrans ? r0 + (idx % (TR / 4)) * 4 : r0 + idx / (BK / 4);
     const int64_t k = kTrans ? k0 + idx / (TR / 4) : k0 + (idx % (BK / 4)) * 4;
     const int64_t off = kTrans ? k * o.ld + r : r * o.ld + k;
-    f32x4 v;
     if constexpr (kVec) {
-      const bool ok = r < o.rows && k < Kd;
-      v = *reinterpret_cast<const f32x4*>(o.p + (ok ? off : 0));
-      if (!ok) v = f32x4{0.f, 0.f, 0.f, 0.f};
+      const bool in = r < o.rows && k < Kd;
+      pre[q] = *reinterpret_cast<const f32x4*>(o.p + (in ? off : 0));
+      ok |= in ? 0xFu << (4 * q) : 0u;
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const bool ok = kTrans ? (r + e < o.rows && k < Kd) : (r < o.rows && k + e < Kd);
-        const float x = o.p[ok ? off + e : 0];
-        v[e] = ok ? x : 0.0f;
+        const bool in = kTrans ? (r + e < o.rows && k < Kd) : (r < o.rows && k + e < Kd);
+        pre[q][e] = o.p[in ? off + e : 0];
+        ok |= in ? 1u << (4 * q + e) : 0u;
       }
     }
-    pre[q] = v;
   }
 }
 
 template <int TR, int BK, bool trans>
-__device__ __forceinline__ void store_op(float* s, int tid, const f32x4 (&pre)[TR * BK / 4 / kThreads]) {
+__device__ __forceinline__ void store_op(float* s, int tid, f32x4 (&pre)[TR * BK / 4 / kThreads], uint32_t ok) {
   constexpr int NQ = TR * BK / 4 / kThreads;
   constexpr int P = BK + 2;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pre[q][e] = (ok >> (4 * q + e)) & 1u ? pre[q][e] : 0.0f;
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     const int idx = q * kThreads + tid;
@@ -121,18 +126,19 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(int64_t M, int64_t N
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
   f32x4 pa[QA], pb[QB];
+  uint32_t oka = 0, okb = 0;
   if (kb < ke) {
-    load_op<TM, BK, kVec, kTA>(a, i0, kb, Kd, tid, pa);
-    load_op<TN, BK, kVec, kTB>(b, j0, kb, Kd, tid, pb);
+    load_op<TM, BK, kVec, kTA>(a, i0, kb, Kd, tid, pa, oka);
+    load_op<TN, BK, kVec, kTB>(b, j0, kb, Kd, tid, pb, okb);
   }
   for (int64_t k0 = kb; k0 < ke; k0 += BK) {
     __syncthreads();
-    store_op<TM, BK, kTA>(sA, tid, pa);
-    store_op<TN, BK, kTB>(sB, tid, pb);
+    store_op<TM, BK, kTA>(sA, tid, pa, oka);
+    store_op<TN, BK, kTB>(sB, tid, pb, okb);
     __syncthreads();
     if (k0 + BK < ke) {
-      load_op<TM, BK, kVec, kTA>(a, i0, k0 + BK, Kd, tid, pa);
-      load_op<TN, BK, kVec, kTB>(b, j0, k0 + BK, Kd, tid, pb);
+      load_op<TM, BK, kVec, kTA>(a, i0, k0 + BK, Kd, tid, pa, oka);
+      load_op<TN, BK, kVec, kTB>(b, j0, k0 + BK, Kd, tid, pb, okb);
     }
 #pragma unroll
     for (int kk = 0; kk < BK / 2; ++kk) {
@@ -164,10 +170,11 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(int64_t M, int64_t N
       float* cp = C + (rbase + i * 32) * ldc + col;
       float cv[16];
       if (beta != 0.0f) {
+        // branch-free: out-of-range lanes read C[0][0] (their value is not stored)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int64_t row = rbase + i * 32 + 8 * (v >> 2) + (v & 3);
-          cv[v] = (row < M && col < N) ? cp[(8 * (v >> 2) + (v & 3)) * ldc] : 0.0f;
+          cv[v] = *((row < M && col < N) ? cp + (8 * (v >> 2) + (v & 3)) * ldc : C);
         }
       }
 #pragma unroll
