@@ -61,19 +61,31 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   return b;
 }
 
-// Element i of an fp32 / fp16 / bf16 array as float.  Branch-free, one
-// dword load: the aligned 32-bit word that holds the element (a 16-bit
-// element is its low or high half; that word lies inside the allocation,
-// whose base is 256-byte aligned and whose size is a multiple of 4).  A
-// branch on the dtype around the load made the compiler wait for each such
-// load before issuing the next one.
-__device__ __forceinline__ float load_elem(const void* p, int64_t i, int dtype) {
-  const bool f32 = dtype == GPTQ_F32;
-  const uintptr_t addr = reinterpret_cast<uintptr_t>(p) + static_cast<uintptr_t>(f32 ? 4 * i : 2 * i);
-  const uint32_t w = *reinterpret_cast<const uint32_t*>(addr & ~static_cast<uintptr_t>(3));
-  const uint16_t h = static_cast<uint16_t>((addr & 2) ? (w >> 16) : w);
+// Element i of an fp32 / fp16 / bf16 array, in two parts so that a caller can
+// issue the load early and convert where the value is used: elem_word loads
+// the aligned 32-bit word that holds the element (a 16-bit element is its low
+// or high half, `hi`; that word lies inside the allocation, whose base is
+// 256-byte aligned and whose size is a multiple of 4) with plain pointer
+// arithmetic from p, so the load stays a global (not flat) load; elem_value
+// converts.  Both are branch-free: a branch on the dtype around the load, a
+// flat load, or a conversion right after the load each made the compiler wait
+// for the load before issuing the next ones.
+__device__ __forceinline__ uint32_t elem_word(const void* p, int64_t i, int dtype, bool& hi) {
+  const char* b = static_cast<const char*>(p);
+  const int64_t off = dtype == GPTQ_F32 ? 4 * i : 2 * i;
+  const int mis = static_cast<int>((reinterpret_cast<uintptr_t>(b) + static_cast<uintptr_t>(off)) & 3u);
+  hi = (mis & 2) != 0;
+  return *reinterpret_cast<const uint32_t*>(b + (off - mis));
+}
+__device__ __forceinline__ float elem_value(uint32_t w, bool hi, int dtype) {
+  const uint16_t h = static_cast<uint16_t>(hi ? (w >> 16) : w);
   const float v16 = dtype == GPTQ_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
-  return f32 ? __builtin_bit_cast(float, w) : v16;
+  return dtype == GPTQ_F32 ? __builtin_bit_cast(float, w) : v16;
+}
+__device__ __forceinline__ float load_elem(const void* p, int64_t i, int dtype) {
+  bool hi;
+  const uint32_t w = elem_word(p, i, dtype, hi);
+  return elem_value(w, hi, dtype);
 }
 __device__ __forceinline__ void store_elem(void* p, int64_t i, int dtype, float v) {
   if (dtype == GPTQ_F32) {

@@ -195,7 +195,7 @@ __global__ __launch_bounds__(256) void gemv_k(LinArgs a) {
           dw[r][4 * v] = t[0]; dw[r][4 * v + 1] = t[1]; dw[r][4 * v + 2] = t[2]; dw[r][4 * v + 3] = t[3];
         }
       }
-      const int64_t g = (c * CB) / a.gs;
+      const int64_t g = static_cast<int>(c * CB) / a.gs;  // 32-bit division (K < 2^31)
       float sc[kRB], zc[kRB];
 #pragma unroll
       for (int r = 0; r < kRB; ++r) {
@@ -640,7 +640,7 @@ __global__ __launch_bounds__(256) void dq_mfma_k(LinArgs a) {
     xs_acc[t] = 0.0f;
   }
   const float magic_fix = Magic<BITS, BF16>::kOffset;
-  int64_t g_cur = ks0 < ks1 ? (ks0 * 32) / a.gs : 0;
+  int64_t g_cur = ks0 < ks1 ? static_cast<int>(ks0 * 32) / a.gs : 0;
 
   auto fold = [&](int64_t g) {
     float s[4], z[4];
@@ -663,7 +663,7 @@ __global__ __launch_bounds__(256) void dq_mfma_k(LinArgs a) {
 
   for (int64_t ks = ks0; ks < ks1; ++ks) {
     const int64_t k0 = ks * 32;
-    const int64_t g = k0 / a.gs;
+    const int64_t g = static_cast<int>(k0) / a.gs;
     if (g != g_cur) {
       fold(g_cur);
       g_cur = g;
@@ -809,7 +809,8 @@ template <int BITS, int NT, int MT>
 struct DsBlock {
   static constexpr int XB = MT == 16 ? 4 : 1;
   uint32_t cw[NT / 16][BITS];
-  float s[NT / 16], z[NT / 16];
+  uint32_t sw[NT / 16], zw[NT / 16];  // words holding the scales and zeros (converted when used)
+  bool sh[NT / 16], zh[NT / 16];
   uint4 x[XB][MT / 16];
 };
 
@@ -852,7 +853,7 @@ __global__ __launch_bounds__(64 * WAVES) void dq_split_k(LinArgs a) {
   // lane (r16, oct): chunk oct (codes 32 oct .. + 31 of the block) of rows 16 i + r16
   auto load = [&](int b, DsBlock<BITS, NT, MT>& L) {
     const int64_t k = static_cast<int64_t>(b) * 128 + 32 * oct;
-    const int64_t g = k / a.gs;
+    const int64_t g = static_cast<int>(k) / a.gs;  // 32-bit division (K < 2^31)
 #pragma unroll
     for (int i = 0; i < BN; ++i) {
       const uint32_t* src = reinterpret_cast<const uint32_t*>(wrow[i] + k * BITS / 8);
@@ -869,8 +870,8 @@ __global__ __launch_bounds__(64 * WAVES) void dq_split_k(LinArgs a) {
       } else {
         L.cw[i][0] = src[0]; L.cw[i][1] = src[1]; L.cw[i][2] = src[2];
       }
-      L.s[i] = load_elem(a.scales, wn[i] * a.ngroups + g, a.sz_dtype);
-      L.z[i] = load_elem(a.zeros, wn[i] * a.ngroups + g, a.sz_dtype);
+      L.sw[i] = elem_word(a.scales, wn[i] * a.ngroups + g, a.sz_dtype, L.sh[i]);
+      L.zw[i] = elem_word(a.zeros, wn[i] * a.ngroups + g, a.sz_dtype, L.zh[i]);
     }
     // B fragments: lane (r16, oct) holds X row 16 j + r16, columns 32 kk + 8 oct .. + 7
     if constexpr (BM == 1) {
@@ -891,7 +892,8 @@ __global__ __launch_bounds__(64 * WAVES) void dq_split_k(LinArgs a) {
 #pragma unroll
     for (int i = 0; i < BN; ++i) {
       uint32_t d[16];
-      dq_chunk<BITS, BF16>(L.cw[i], L.s[i], L.z[i], d, std::make_integer_sequence<int, 16>{});
+      dq_chunk<BITS, BF16>(L.cw[i], elem_value(L.sw[i], L.sh[i], a.sz_dtype), elem_value(L.zw[i], L.zh[i], a.sz_dtype),
+                           d, std::make_integer_sequence<int, 16>{});
       uint4* dst = reinterpret_cast<uint4*>(tile + r16 * P + 32 * oct);
 #pragma unroll
       for (int q = 0; q < 4; ++q) dst[q] = uint4{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
@@ -1054,7 +1056,7 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
     uint4 xb[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) xb[kk] = xok ? perm_0415(L.x[kk]) : uint4{0u, 0u, 0u, 0u};
-    const int g = static_cast<int>((static_cast<int64_t>(b) * 128 + 32 * g4) / a.gs);
+    const int g = (b * 128 + 32 * g4) / a.gs;  // 32-bit division (K < 2^31)
     if constexpr (kFold) {
       f32x4 sx = f32x4{0.f, 0.f, 0.f, 0.f};
       const uint4 ones = uint4{0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};
@@ -1171,23 +1173,34 @@ int launch_reg4(hipStream_t st, const LinArgs& a) {
   return check_launch("dq_reg4");
 }
 
-// Large products (M > 16 and at least 128 output tiles): one workgroup per
-// 128 x MT tile of (weight rows x activation rows), K in steps of 64.  Each
-// thread loads one 32-code chunk of one weight row per step, dequantises it
-// into a double-buffered LDS tile, and stages a piece of X beside it; the 4
-// waves (2 x 2) multiply 32x32x16 MFMA fragments from LDS.  The next step's
-// codes and X are in registers while the current step is multiplied.
-template <int MT>
+// Large products (M > 16 and enough output tiles): one workgroup per NT x MT
+// tile of (weight rows x activation rows), NT = 128 (K in steps of 64) or 64
+// (steps of 128) so that the grid fills the GPU.  Each thread loads one
+// 32-code chunk of one weight row per step, dequantises it into a
+// double-buffered LDS tile, and stages a piece of X beside it; the 4 waves
+// (2 x 2) multiply 32x32x16 MFMA fragments from LDS.  The codes and X of the
+// next two steps are in registers while the current step is multiplied.
+template <int NT, int MT>
 struct DtCfg {
-  static constexpr int NT = 128, KB = 64, CPR = KB / 32;
-  static constexpr int P = KB + 8;               // LDS row pitch (halves): 144 B, conflict-free fragment reads
+  static constexpr int KB = 8192 / NT, CPR = KB / 32;  // 256 chunks of 32 codes per step
+  static constexpr int P = KB + 8;               // LDS row pitch (halves): conflict-free fragment reads
   static constexpr int XV = MT * KB / 8 / 256;   // 16-byte X pieces per thread and step
 };
 
-template <int BITS, bool BF16, int MT>
+template <int BITS, int XV>
+struct DtStage {
+  uint32_t cw[BITS];
+  uint32_t csw, czw;  // words holding the scale and zero (converted when stored)
+  bool csh, czh;
+  uint4 xr[XV];
+  uint32_t xok;  // bit v: X piece v lies inside X
+};
+
+template <int BITS, bool BF16, int NT, int MT>
 __global__ __launch_bounds__(256) void dq_tile_k(LinArgs a) {
-  using C = DtCfg<MT>;
-  constexpr int NT = C::NT, KB = C::KB, P = C::P, XV = C::XV;
+  using C = DtCfg<NT, MT>;
+  constexpr int KB = C::KB, P = C::P, XV = C::XV;
+  static_assert(XV <= 32, "validity bits");
   __shared__ __attribute__((aligned(16))) uint16_t sW[2][NT * P];
   __shared__ __attribute__((aligned(16))) uint16_t sX[2][MT * P];
   const int tid = threadIdx.x;
@@ -1200,52 +1213,58 @@ __global__ __launch_bounds__(256) void dq_tile_k(LinArgs a) {
   const int wr = tid / C::CPR, wc = tid % C::CPR;
   const int64_t wn = std::min<int64_t>(n0 + wr, a.N - 1);
   const uint8_t* wrow = a.packed + wn * a.pitch;
-  uint32_t cw[BITS];
-  float cs = 0.0f, cz = 0.0f;
-  uint4 xr[XV];
-  auto load = [&](int step) {
+  using St = DtStage<BITS, XV>;
+  // loads are branch-free (rows past M read row 0 and are zeroed when stored)
+  // so that a stage's loads stay in flight across the multiply
+  auto load = [&](int step, St& R) {
     const int64_t k = static_cast<int64_t>(step) * KB + 32 * wc;
     const uint32_t* src = reinterpret_cast<const uint32_t*>(wrow + k * BITS / 8);
     if constexpr (BITS == 4) {
       const uint4 v = *reinterpret_cast<const uint4*>(src);
-      cw[0] = v.x; cw[1] = v.y; cw[2] = v.z; cw[3] = v.w;
+      R.cw[0] = v.x; R.cw[1] = v.y; R.cw[2] = v.z; R.cw[3] = v.w;
     } else if constexpr (BITS == 8) {
       const uint4 v0 = reinterpret_cast<const uint4*>(src)[0], v1 = reinterpret_cast<const uint4*>(src)[1];
-      cw[0] = v0.x; cw[1] = v0.y; cw[2] = v0.z; cw[3] = v0.w; cw[4] = v1.x; cw[5] = v1.y; cw[6] = v1.z; cw[7] = v1.w;
+      R.cw[0] = v0.x; R.cw[1] = v0.y; R.cw[2] = v0.z; R.cw[3] = v0.w;
+      R.cw[4] = v1.x; R.cw[5] = v1.y; R.cw[6] = v1.z; R.cw[7] = v1.w;
     } else if constexpr (BITS == 2) {
       const uint2 v = *reinterpret_cast<const uint2*>(src);
-      cw[0] = v.x; cw[1] = v.y;
+      R.cw[0] = v.x; R.cw[1] = v.y;
     } else {
-      cw[0] = src[0]; cw[1] = src[1]; cw[2] = src[2];
+      R.cw[0] = src[0]; R.cw[1] = src[1]; R.cw[2] = src[2];
     }
-    const int64_t g = k / a.gs;
-    cs = load_elem(a.scales, wn * a.ngroups + g, a.sz_dtype);
-    cz = load_elem(a.zeros, wn * a.ngroups + g, a.sz_dtype);
+    // a 64-bit division here is a divergent branch that made the compiler wait for the loads
+    const int64_t g = static_cast<int>(k) / a.gs;
+    R.csw = elem_word(a.scales, wn * a.ngroups + g, a.sz_dtype, R.csh);
+    R.czw = elem_word(a.zeros, wn * a.ngroups + g, a.sz_dtype, R.czh);
+    R.xok = 0;
 #pragma unroll
     for (int v = 0; v < XV; ++v) {
       const int e = tid + 256 * v;
       const int64_t m = m0 + e / (KB / 8);
-      xr[v] = m < a.M ? *reinterpret_cast<const uint4*>(a.x + m * a.K + static_cast<int64_t>(step) * KB +
-                                                         8 * (e % (KB / 8)))
-                      : uint4{0u, 0u, 0u, 0u};
+      const bool in = m < a.M;
+      R.xr[v] = *reinterpret_cast<const uint4*>(a.x + (in ? m : 0) * a.K + static_cast<int64_t>(step) * KB +
+                                                8 * (e % (KB / 8)));
+      R.xok |= in ? 1u << v : 0u;
     }
   };
-  auto store = [&](int buf) {
+  auto store = [&](int buf, const St& R) {
     uint32_t d[16];
-    dq_chunk<BITS, BF16>(cw, cs, cz, d, std::make_integer_sequence<int, 16>{});
+    dq_chunk<BITS, BF16>(R.cw, elem_value(R.csw, R.csh, a.sz_dtype), elem_value(R.czw, R.czh, a.sz_dtype), d,
+                         std::make_integer_sequence<int, 16>{});
     uint4* dst = reinterpret_cast<uint4*>(&sW[buf][wr * P + 32 * wc]);
 #pragma unroll
     for (int q = 0; q < 4; ++q) dst[q] = uint4{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
 #pragma unroll
     for (int v = 0; v < XV; ++v) {
       const int e = tid + 256 * v;
-      *reinterpret_cast<uint4*>(&sX[buf][(e / (KB / 8)) * P + 8 * (e % (KB / 8))]) = xr[v];
+      *reinterpret_cast<uint4*>(&sX[buf][(e / (KB / 8)) * P + 8 * (e % (KB / 8))]) =
+          (R.xok >> v) & 1u ? R.xr[v] : uint4{0u, 0u, 0u, 0u};
     }
   };
 
-  // waves 2 x 2: 64 weight rows x MT / 2 activation rows each, 32 x 32 blocks
-  constexpr int BN = 2, BM = MT / 64;
-  const int wbase = 64 * (wave >> 1), mbase = (MT / 2) * (wave & 1);
+  // waves 2 x 2: NT / 2 weight rows x MT / 2 activation rows each, 32 x 32 blocks
+  constexpr int BN = NT / 64, BM = MT / 64;
+  const int wbase = (NT / 2) * (wave >> 1), mbase = (MT / 2) * (wave & 1);
   f32x16 acc[BN][BM];
 #pragma unroll
   for (int i = 0; i < BN; ++i)
@@ -1277,17 +1296,22 @@ __global__ __launch_bounds__(256) void dq_tile_k(LinArgs a) {
     }
   };
 
-  load(0);
-  store(0);
-  if (nsteps > 1) load(1);
+  // two register stages: the loads of step s + 2 are issued before step s is
+  // multiplied, so each has two steps of multiply to land before its store
+  St R0, R1;
+  load(0, R0);
+  if (nsteps > 1) load(1, R1);
+  store(0, R0);
   __syncthreads();
-  for (int step = 0; step < nsteps; ++step) {
-    const int buf = step & 1;
-    compute(buf);
-    if (step + 1 < nsteps) {
-      store(buf ^ 1);
-      if (step + 2 < nsteps) load(step + 2);
-    }
+  for (int step = 0; step < nsteps; step += 2) {
+    if (step + 2 < nsteps) load(step + 2, R0);
+    compute(0);
+    if (step + 1 < nsteps) store(1, R1);
+    __syncthreads();
+    if (step + 1 >= nsteps) break;
+    if (step + 3 < nsteps) load(step + 3, R1);
+    compute(1);
+    if (step + 2 < nsteps) store(0, R0);
     __syncthreads();
   }
   // 32x32 layout: lane l, register v -> W row 8 (v / 4) + 4 (l / 32) + v % 4, X row l % 32
@@ -1317,7 +1341,8 @@ int launch_split(hipStream_t st, const LinArgs& a) {
 
 // M <= 16: split-K with 16 waves, weight rows per workgroup chosen so that
 // the grid stays >= 256 workgroups while X is re-read by fewer of them;
-// M > 16: the tiled kernel when it has >= 128 tiles, else split-K
+// M > 16: the tiled kernel with 128-row tiles when there are >= 256 of them,
+// 64-row tiles when there are >= 128, else split-K
 template <int BITS, bool BF16>
 int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
   if constexpr (BITS == 4 && !BF16) {
@@ -1335,12 +1360,14 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
     return launch_split<BITS, BF16, 16, 16, 16>(st, a);
   }
   const int64_t mt = a.M <= 64 ? 64 : 128;
-  if (cdiv(a.N, 128) * cdiv(a.M, mt) >= 128) {
-    const dim3 grid(static_cast<unsigned>(cdiv(a.N, 128)), static_cast<unsigned>(cdiv(a.M, mt)));
-    if (mt == 64)
-      hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 64>), grid, dim3(256), 0, st, a);
-    else
-      hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 128>), grid, dim3(256), 0, st, a);
+  const int64_t t128 = cdiv(a.N, 128) * cdiv(a.M, mt), t64 = cdiv(a.N, 64) * cdiv(a.M, mt);
+  if (t128 >= 256 || t64 >= 128) {
+    const bool wide = t128 >= 256;
+    const dim3 grid(static_cast<unsigned>(cdiv(a.N, wide ? 128 : 64)), static_cast<unsigned>(cdiv(a.M, mt)));
+    if (wide && mt == 64) hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 128, 64>), grid, dim3(256), 0, st, a);
+    else if (wide) hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 128, 128>), grid, dim3(256), 0, st, a);
+    else if (mt == 64) hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 64, 64>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 64, 128>), grid, dim3(256), 0, st, a);
     return check_launch("dq_tile");
   }
   if (a.M <= 64) return launch_split<BITS, BF16, 32, 64, 8>(st, a);
@@ -1463,6 +1490,7 @@ extern "C" int gptq_linear(const void* x, int x_dtype, int64_t M, const uint8_t*
   GPTQ_REQUIRE(M >= 0 && N > 0 && K > 0 && ngroups > 0 && (g_idx || group_size > 0), GPTQ_ERR_SHAPE,
                "linear: bad shape");
   GPTQ_REQUIRE(g_idx || cdiv(K, group_size) <= ngroups, GPTQ_ERR_SHAPE, "linear: too few groups");
+  GPTQ_REQUIRE(K <= INT32_MAX / 8, GPTQ_ERR_SHAPE, "linear: K=%lld too large", static_cast<long long>(K));
   if (M == 0) return GPTQ_OK;
   hipStream_t st = as_hip(stream);
   const int eb = bits == 0 ? 8 : bits;
