@@ -69,9 +69,11 @@ class Block:
         self.hkey = {"q_proj": "qkv", "k_proj": "qkv", "v_proj": "qkv", "o_proj": "o", "gate_proj": "up",
                      "up_proj": "up", "down_proj": "down"}
 
-        # fused projections for the forward (the GPTQ layers stay separate)
+        # fused q/k/v projection for the forward (the GPTQ layers stay separate);
+        # gate and up stay two products so that SiLU and the product run on
+        # contiguous tensors (on column slices of one fused output they take
+        # torch's strided elementwise path)
         self.wqkv = torch.cat([self.w["q_proj"], self.w["k_proj"], self.w["v_proj"]], 0)
-        self.wgu = torch.cat([self.w["gate_proj"], self.w["up_proj"]], 0)
         self.gqa = None
 
     @staticmethod
@@ -137,8 +139,8 @@ class Block:
             h = torch.add(zc, F.linear(o_in.view(b, T, HID), self.w["o_proj"]))
             x2 = bufs["up"][r0:r1].view(b, T, HID)
             self.rmsnorm_into(torch, F, h, self.g2, x2)
-            g_, u_ = F.linear(x2, self.wgu).split(FFN, dim=-1)
-            torch.mul(F.silu(g_), u_, out=bufs["down"][r0:r1].view(b, T, FFN))
+            g_ = F.silu(F.linear(x2, self.w["gate_proj"]), inplace=True)
+            torch.mul(g_, F.linear(x2, self.w["up_proj"]), out=bufs["down"][r0:r1].view(b, T, FFN))
 
 
 def hessian_flops(n, K):
@@ -376,7 +378,7 @@ def main():
     ap.add_argument("--bits", type=int, default=4)
     ap.add_argument("--nseq", type=int, default=128)
     ap.add_argument("--seqlen", type=int, default=2048)
-    ap.add_argument("--chunk", type=int, default=8, help="sequences per forward chunk")
+    ap.add_argument("--chunk", type=int, default=16, help="sequences per forward chunk")
     ap.add_argument("--hessian-groups", type=int, default=1,
                     help="forward groups whose Hessian accumulation overlaps the next group's forward")
     ap.add_argument("--no-cpu", action="store_true")
