@@ -1180,11 +1180,13 @@ int launch_reg4(hipStream_t st, const LinArgs& a) {
 // double-buffered LDS tile, and stages a piece of X beside it; the 4 waves
 // (2 x 2) multiply 32x32x16 MFMA fragments from LDS.  The codes and X of the
 // next two steps are in registers while the current step is multiplied.
-template <int NT, int MT>
+template <int NT, int MT, int KB_>
 struct DtCfg {
-  static constexpr int KB = 8192 / NT, CPR = KB / 32;  // 256 chunks of 32 codes per step
+  static constexpr int KB = KB_, CPR = KB / 32;  // NT * CPR <= 256 chunks of 32 codes per step
+  static constexpr int CW = NT * CPR / 64;       // waves that load and dequantise codes
   static constexpr int P = KB + 8;               // LDS row pitch (halves): conflict-free fragment reads
   static constexpr int XV = MT * KB / 8 / 256;   // 16-byte X pieces per thread and step
+  static_assert(NT * CPR <= 256 && (NT * CPR) % 64 == 0, "code chunks per step");
 };
 
 template <int BITS, int XV>
@@ -1196,21 +1198,22 @@ struct DtStage {
   uint32_t xok;  // bit v: X piece v lies inside X
 };
 
-template <int BITS, bool BF16, int NT, int MT>
+template <int BITS, bool BF16, int NT, int MT, int KB_>
 __global__ __launch_bounds__(256) void dq_tile_k(LinArgs a) {
-  using C = DtCfg<NT, MT>;
+  using C = DtCfg<NT, MT, KB_>;
   constexpr int KB = C::KB, P = C::P, XV = C::XV;
   static_assert(XV <= 32, "validity bits");
   __shared__ __attribute__((aligned(16))) uint16_t sW[2][NT * P];
   __shared__ __attribute__((aligned(16))) uint16_t sX[2][MT * P];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * NT;
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * MT;
   const int nsteps = static_cast<int>(a.K / KB);
+  const bool coder = wave < C::CW;  // wave-uniform: this wave loads and dequantises codes
 
-  const int wr = tid / C::CPR, wc = tid % C::CPR;
+  const int wr = (tid / C::CPR) % NT, wc = tid % C::CPR;
   const int64_t wn = std::min<int64_t>(n0 + wr, a.N - 1);
   const uint8_t* wrow = a.packed + wn * a.pitch;
   using St = DtStage<BITS, XV>;
@@ -1219,7 +1222,8 @@ __global__ __launch_bounds__(256) void dq_tile_k(LinArgs a) {
   auto load = [&](int step, St& R) {
     const int64_t k = static_cast<int64_t>(step) * KB + 32 * wc;
     const uint32_t* src = reinterpret_cast<const uint32_t*>(wrow + k * BITS / 8);
-    if constexpr (BITS == 4) {
+    if (!coder) {
+    } else if constexpr (BITS == 4) {
       const uint4 v = *reinterpret_cast<const uint4*>(src);
       R.cw[0] = v.x; R.cw[1] = v.y; R.cw[2] = v.z; R.cw[3] = v.w;
     } else if constexpr (BITS == 8) {
@@ -1234,8 +1238,10 @@ __global__ __launch_bounds__(256) void dq_tile_k(LinArgs a) {
     }
     // a 64-bit division here is a divergent branch that made the compiler wait for the loads
     const int64_t g = static_cast<int>(k) / a.gs;
-    R.csw = elem_word(a.scales, wn * a.ngroups + g, a.sz_dtype, R.csh);
-    R.czw = elem_word(a.zeros, wn * a.ngroups + g, a.sz_dtype, R.czh);
+    if (coder) {
+      R.csw = elem_word(a.scales, wn * a.ngroups + g, a.sz_dtype, R.csh);
+      R.czw = elem_word(a.zeros, wn * a.ngroups + g, a.sz_dtype, R.czh);
+    }
     R.xok = 0;
 #pragma unroll
     for (int v = 0; v < XV; ++v) {
@@ -1248,12 +1254,14 @@ __global__ __launch_bounds__(256) void dq_tile_k(LinArgs a) {
     }
   };
   auto store = [&](int buf, const St& R) {
-    uint32_t d[16];
-    dq_chunk<BITS, BF16>(R.cw, elem_value(R.csw, R.csh, a.sz_dtype), elem_value(R.czw, R.czh, a.sz_dtype), d,
-                         std::make_integer_sequence<int, 16>{});
-    uint4* dst = reinterpret_cast<uint4*>(&sW[buf][wr * P + 32 * wc]);
+    if (coder) {
+      uint32_t d[16];
+      dq_chunk<BITS, BF16>(R.cw, elem_value(R.csw, R.csh, a.sz_dtype), elem_value(R.czw, R.czh, a.sz_dtype), d,
+                           std::make_integer_sequence<int, 16>{});
+      uint4* dst = reinterpret_cast<uint4*>(&sW[buf][wr * P + 32 * wc]);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dst[q] = uint4{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
+      for (int q = 0; q < 4; ++q) dst[q] = uint4{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
+    }
 #pragma unroll
     for (int v = 0; v < XV; ++v) {
       const int e = tid + 256 * v;
@@ -1364,10 +1372,14 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
   if (t128 >= 256 || t64 >= 128) {
     const bool wide = t128 >= 256;
     const dim3 grid(static_cast<unsigned>(cdiv(a.N, wide ? 128 : 64)), static_cast<unsigned>(cdiv(a.M, mt)));
-    if (wide && mt == 64) hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 128, 64>), grid, dim3(256), 0, st, a);
-    else if (wide) hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 128, 128>), grid, dim3(256), 0, st, a);
-    else if (mt == 64) hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 64, 64>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 64, 128>), grid, dim3(256), 0, st, a);
+    if (wide && mt == 64) hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 128, 64, 64>), grid, dim3(256), 0, st, a);
+    else if (wide) hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 128, 128, 64>), grid, dim3(256), 0, st, a);
+    // 64-row tiles: 128-column steps while one workgroup per CU is all the grid
+    // gives; 64-column steps (half the LDS) when two fit per CU and are needed
+    else if (t64 <= 256 && mt == 64) hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 64, 64, 128>), grid, dim3(256), 0, st, a);
+    else if (t64 <= 256) hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 64, 128, 128>), grid, dim3(256), 0, st, a);
+    else if (mt == 64) hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 64, 64, 64>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 64, 128, 64>), grid, dim3(256), 0, st, a);
     return check_launch("dq_tile");
   }
   if (a.M <= 64) return launch_split<BITS, BF16, 32, 64, 8>(st, a);

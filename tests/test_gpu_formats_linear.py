@@ -230,9 +230,10 @@ def test_triton_quantized_linear(hip):
 @pytest.mark.parametrize("bits", [3, 4])
 @pytest.mark.parametrize("M,N,K,gs", [(16, 4101, 4096, 128), (9, 1000, 1024, 32), (64, 2050, 2048, 128),
                                       (100, 1027, 4096, 64), (128, 4096, 4096, 128),
-                                      # tiled kernel: 64-row tiles (odd step count), 128-row tiles
-                                      (40, 8200, 512, 128), (128, 8256, 384, 128), (130, 16448, 256, 128),
-                                      (64, 32832, 256, 128)])
+                                      # tiled kernel: 64-row tiles with 128-column steps (odd step
+                                      # count) and with 64-column steps, 128-row tiles
+                                      (40, 8200, 512, 128), (128, 8256, 384, 128), (64, 16448, 384, 128),
+                                      (100, 16448, 640, 128), (130, 16448, 256, 128), (64, 32832, 256, 128)])
 def test_linear_dequant_gemm(hip, xdt, bits, M, N, K, gs):
     """M > 4: dequantise-then-MFMA kernels (split-K and tiled), ragged N and M,
     groups of 32-128 (one group per 32-code chunk), bias."""
