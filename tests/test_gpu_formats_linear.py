@@ -245,3 +245,26 @@ def test_linear_dequant_gemm(hip, xdt, bits, M, N, K, gs):
     ref = O.linear(x.float().numpy(), codes, scales.numpy(), zeros.numpy(), np.arange(K) // gs, bias.float().numpy())
     err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
     assert err < TOL[xdt], err
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,N", [(1, 1030), (3, 1030), (16, 4101), (128, 8256)])
+def test_linear_scales_at_odd_offset(hip, xdt, M, N):
+    """Scales and zeros whose base is 2 but not 4-byte aligned (a contiguous
+    view one element into its storage): the kernels read the aligned word
+    holding each 16-bit element and must give exactly the aligned result."""
+    from distributed_gptq_amd import _ops
+    K, gs, bits = 1024, 128, 4
+    codes, scales, zeros, x = _case(M, N, K, bits, gs, 7 + M, xdt)
+    packed = torch.from_numpy(O.pack_bitstream(codes, bits)).cuda()
+    s_al, z_al = scales.cuda(), zeros.cuda()
+    s_buf = torch.zeros(scales.numel() + 1, dtype=scales.dtype, device="cuda")
+    z_buf = torch.zeros(zeros.numel() + 1, dtype=zeros.dtype, device="cuda")
+    s_odd, z_odd = s_buf[1:].view(scales.shape), z_buf[1:].view(zeros.shape)
+    s_odd.copy_(s_al)
+    z_odd.copy_(z_al)
+    assert s_odd.data_ptr() % 4 == 2 and z_odd.data_ptr() % 4 == 2
+    xc = x.cuda()
+    y_al = _ops.linear(xc, packed, bits, s_al, z_al, K, group_size=gs)
+    y_odd = _ops.linear(xc, packed, bits, s_odd, z_odd, K, group_size=gs)
+    assert torch.equal(y_al, y_odd)
