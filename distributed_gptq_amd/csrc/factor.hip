@@ -66,14 +66,15 @@ __device__ __forceinline__ float damped(const float* H, int64_t K, float scale, 
 __global__ void build_A(const float* __restrict__ H, int64_t K, float scale, const int32_t* __restrict__ perm,
                         int fix_dead, const float* __restrict__ lam, float* __restrict__ A,
                         float* __restrict__ Hd) {
+  // rows over blockIdx.y, columns over threads: no 64-bit division per element
   const float l = lam[0];
-  const int64_t total = K * K;
-  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
-       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t i = idx / K, j = idx - (idx / K) * K;
-    if (Hd) Hd[idx] = damped(H, K, scale, perm, fix_dead != 0, l, i, j);
-    if (i >= j) A[idx] = damped(H, K, scale, perm, fix_dead != 0, l, K - 1 - i, K - 1 - j);
-  }
+  for (int64_t i = blockIdx.y; i < K; i += gridDim.y)
+    for (int64_t j = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; j < K;
+         j += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+      const int64_t idx = i * K + j;
+      if (Hd) Hd[idx] = damped(H, K, scale, perm, fix_dead != 0, l, i, j);
+      if (i >= j) A[idx] = damped(H, K, scale, perm, fix_dead != 0, l, K - 1 - i, K - 1 - j);
+    }
 }
 
 __global__ void fill_zero(float* __restrict__ p, int64_t n) {
@@ -408,8 +409,9 @@ extern "C" int gptq_damp_factor(const float* H, int64_t K, float scale, float pe
   hipLaunchKernelGGL(diag_stats, dim3(1), dim3(1024), 0, st, H, K, scale, percdamp, dead_cols, lam, info);
   int rc = check_launch("diag_stats");
   if (rc) return rc;
-  hipLaunchKernelGGL(build_A, dim3(grid_for(K * K, 256)), dim3(256), 0, st, H, K, scale, perm, dead_cols ? 1 : 0, lam,
-                     A, Hd);
+  hipLaunchKernelGGL(build_A, dim3(static_cast<unsigned>(std::min<int64_t>(cdiv(K, 256), 64)),
+                                  static_cast<unsigned>(std::min<int64_t>(K, 65535))),
+                     dim3(256), 0, st, H, K, scale, perm, dead_cols ? 1 : 0, lam, A, Hd);
   if ((rc = check_launch("build_A"))) return rc;
   hipLaunchKernelGGL(fill_zero, dim3(grid_for(K * K, 256)), dim3(256), 0, st, out, K * K);
   if ((rc = check_launch("fill_zero"))) return rc;

@@ -338,14 +338,33 @@ __global__ __launch_bounds__(64 * kSW) void sweep_r16(SubArgs a) {
 // any of it is written.  Entries of perm outside [0, cols) are skipped.
 constexpr int64_t kUnpermMaxCols = 16384;
 
+// 8 columns per thread and pass, loads branch-free (out-of-range lanes read
+// column 0 and are not stored), so that a thread's loads are in flight
+// together
 template <typename E>
 __device__ __forceinline__ void unpermute_one(E* row, const int32_t* perm, int64_t cols, E* buf) {
-  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
-    const uint32_t o = static_cast<uint32_t>(perm[c]);
-    if (o < static_cast<uint64_t>(cols)) buf[o] = row[c];
+  const int n = static_cast<int>(cols);
+  constexpr int U = 8;
+  for (int c = threadIdx.x; c < n; c += 256 * U) {
+    uint32_t o[U];
+    E v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int cc = c + 256 * u;
+      const bool in = cc < n;
+      o[u] = in ? static_cast<uint32_t>(perm[cc]) : 0xFFFFFFFFu;
+      v[u] = row[in ? cc : 0];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (o[u] < static_cast<uint32_t>(n)) buf[o[u]] = v[u];
   }
   __syncthreads();
-  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) row[c] = buf[c];
+  for (int c = threadIdx.x; c < n; c += 256 * U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (c + 256 * u < n) row[c + 256 * u] = buf[c + 256 * u];
+  }
   __syncthreads();
 }
 
@@ -392,19 +411,15 @@ __global__ void quantize_rows_k(const float* __restrict__ x, int64_t rows, int64
 __global__ void prepare_weight_k(const void* __restrict__ w, int dtype, int64_t rows, int64_t cols, int64_t ldw,
                                  const int32_t* __restrict__ perm, const int32_t* __restrict__ dead, int transpose,
                                  float* __restrict__ out) {
-  const int64_t total = rows * cols;
-  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
-       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t r = idx / cols, c = idx - (idx / cols) * cols;
-    const int64_t pc = perm ? perm[c] : c;
-    float v;
-    if (transpose)
-      v = load_elem(w, pc * ldw + r, dtype);
-    else
-      v = load_elem(w, r * ldw + pc, dtype);
-    if (dead && dead[pc]) v = 0.0f;
-    out[idx] = v;
-  }
+  // rows over blockIdx.y, columns over threads: no 64-bit division per element
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y)
+    for (int64_t c = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; c < cols;
+         c += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+      const int64_t pc = perm ? perm[c] : c;
+      float v = load_elem(w, transpose ? pc * ldw + r : r * ldw + pc, dtype);
+      if (dead && dead[pc]) v = 0.0f;
+      out[r * cols + c] = v;
+    }
 }
 
 int launch_r16(hipStream_t st, const SubArgs& a) {
@@ -473,9 +488,9 @@ extern "C" int gptq_prepare_weight(const void* w, int dtype, int64_t rows, int64
   GPTQ_REQUIRE(valid_dtype(dtype), GPTQ_ERR_DTYPE, "prepare_weight: bad dtype %d", dtype);
   GPTQ_REQUIRE(rows > 0 && cols > 0 && ldw >= (transpose ? rows : cols), GPTQ_ERR_SHAPE,
                "prepare_weight: bad shape");
-  const int64_t total = rows * cols;
-  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(cdiv(total, 256), 65536));
-  hipLaunchKernelGGL(prepare_weight_k, dim3(blocks), dim3(256), 0, as_hip(stream), w, dtype, rows, cols, ldw, perm,
+  const dim3 grid(static_cast<unsigned>(std::min<int64_t>(cdiv(cols, 256), 64)),
+                  static_cast<unsigned>(std::min<int64_t>(rows, 65535)));
+  hipLaunchKernelGGL(prepare_weight_k, grid, dim3(256), 0, as_hip(stream), w, dtype, rows, cols, ldw, perm,
                      dead_cols, transpose, out);
   return check_launch("prepare_weight");
 }
