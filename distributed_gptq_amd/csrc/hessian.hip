@@ -537,7 +537,12 @@ void hessian_tile32(const float* __restrict__ X, int64_t n, int K, int64_t ldx, 
   // per stage: 2 operands x 16 tokens x 64 float4 = 2048 float4, 4 per thread
   constexpr int kPer = 2 * kBK * (kTile / 4) / kThreads;
   f32x4 pre[kPer];
+  uint32_t ok = 0;  // bit 4 q + e: element e of pre[q] lies inside X
+  static_assert(kPer <= 8, "validity bits");
+  // branch-free loads (out-of-range elements read X[0][0] and are zeroed when
+  // stored), so that the stage's loads stay in flight across the multiply
   auto load_stage = [&](int64_t t0) {
+    ok = 0;
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
       const int idx = q * kThreads + tid;
@@ -546,17 +551,20 @@ void hessian_tile32(const float* __restrict__ X, int64_t n, int K, int64_t ldx, 
       const int f4 = idx & 63;
       const int64_t tok = t0 + tok_l;
       const int feat = (op == 0 ? I : J) * kTile + f4 * 4;
-      f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      if (!(diag && op == 1) && tok < t_end && feat < K) {
-        const float* src = X + tok * ldx + feat;
-        if constexpr (kVec) {
-          v = *reinterpret_cast<const f32x4*>(src);
-        } else {
+      const bool row_in = !(diag && op == 1) && tok < t_end;
+      const int64_t off = tok * ldx + feat;
+      if constexpr (kVec) {
+        const bool in = row_in && feat < K;
+        pre[q] = *reinterpret_cast<const f32x4*>(X + (in ? off : 0));
+        ok |= in ? 0xFu << (4 * q) : 0u;
+      } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = (feat + e < K) ? src[e] : 0.0f;
+        for (int e = 0; e < 4; ++e) {
+          const bool in = row_in && feat + e < K;
+          pre[q][e] = X[in ? off + e : 0];
+          ok |= in ? 1u << (4 * q + e) : 0u;
         }
       }
-      pre[q] = v;
     }
   };
   auto store_stage = [&]() {
@@ -565,7 +573,10 @@ void hessian_tile32(const float* __restrict__ X, int64_t n, int K, int64_t ldx, 
       const int idx = q * kThreads + tid;
       const int op = idx >> 10;
       if (diag && op == 1) continue;
-      lds[op][(idx >> 6) & 15][idx & 63] = pre[q];
+      f32x4 v = pre[q];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (ok >> (4 * q + e)) & 1u ? v[e] : 0.0f;
+      lds[op][(idx >> 6) & 15][idx & 63] = v;
     }
   };
 
