@@ -123,16 +123,22 @@ __device__ __forceinline__ void put32(float* pc, int ldc, const f32x16& acc, flo
   for (int v = 0; v < 16; ++v) pc[(8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) * ldc + (lane & 31)] = scale * acc[v];
 }
 
+__device__ __forceinline__ float bperm(int src_lane, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lane * 4, __builtin_bit_cast(int, v)));
+}
+
 // One wave: D (32 x 32 at sD, lower part) = L L^T and X = L^-1, written back
 // over D and into sXd (zeros above).  Lane l holds the 4 x 4 sub-block
 // (rows 4 (l / 8) + u, columns 4 (l % 8) + v) of the working matrix and of
 // Y (initially I).  Step j: the pivot comes from its lane (v_readlane); the
-// lanes holding column j store L's column j, the lanes holding row j store
-// Y's row j scaled by 1 / L[j][j], both in LDS (sc, 64 floats), and every
-// lane reads back what it needs and applies the two rank-1 updates
+// lanes holding column j have L's column j, the lanes holding row j have Y's
+// row j scaled by 1 / L[j][j]; every lane fetches the pieces it needs from
+// them with ds_bpermute and applies the two rank-1 updates
 //   D[r][c] -= L[r][j] L[c][j]  (c > j),   Y[r][c] -= L[r][j] Y[j][c]  (r > j),
-// right-looking Cholesky and forward elimination fused.
-__device__ __forceinline__ void diag32(float* sD, float* sXd, float* sc, int lane, int col0, int lim, int& first_bad) {
+// right-looking Cholesky and forward elimination fused.  (An LDS store, wave
+// barrier and load per step cost 600 cycles a column, most of the leaf.)
+
+__device__ __forceinline__ void diag32(float* sD, float* sXd, int lane, int col0, int lim, int& first_bad) {
   const int ra = lane >> 3, cb = lane & 7;
   float a[4][4], y[4][4];
 #pragma unroll
@@ -142,8 +148,6 @@ __device__ __forceinline__ void diag32(float* sD, float* sXd, float* sc, int lan
       a[u][v] = sD[(4 * ra + u) * kLP + 4 * cb + v];
       y[u][v] = (4 * ra + u == 4 * cb + v) ? 1.0f : 0.0f;
     }
-  float* lcol = sc;
-  float* yrow = sc + 32;
 #pragma unroll
   for (int j = 0; j < kLB; ++j) {
     const int jb = j >> 2, jv = j & 3;
@@ -153,30 +157,29 @@ __device__ __forceinline__ void diag32(float* sD, float* sXd, float* sc, int lan
     // sequential chain of the 32 steps
     const float d = __builtin_amdgcn_sqrtf(piv);
     const float id = __builtin_amdgcn_rcpf(d);
-    if (cb == jb) {
-      f32x4 lv;
+    // column j of L for rows 4 ra + u (kept by the lanes with cb == jb) and
+    // row j of Y for columns 4 cb + v (kept by the lanes with ra == jb);
+    // every lane computes them, the owners' values are broadcast with
+    // ds_bpermute (no LDS round trip or wave barrier on the chain)
+    float lv[4], yv[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int r = 4 * ra + u;
-        lv[u] = r > j ? a[u][jv] * id : (r == j ? d : 0.0f);
-        a[u][jv] = lv[u];
-      }
-      *reinterpret_cast<f32x4*>(lcol + 4 * ra) = lv;
+    for (int u = 0; u < 4; ++u) {
+      const int r = 4 * ra + u;
+      lv[u] = r > j ? a[u][jv] * id : (r == j ? d : 0.0f);
+      if (cb == jb) a[u][jv] = lv[u];
     }
-    if (ra == jb) {
-      f32x4 yv;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        y[jv][v] *= id;
-        yv[v] = y[jv][v];
-      }
-      *reinterpret_cast<f32x4*>(yrow + 4 * cb) = yv;
+    for (int v = 0; v < 4; ++v) {
+      yv[v] = y[jv][v] * id;
+      if (ra == jb) y[jv][v] = yv[v];
     }
-    wave_sync();
-    const f32x4 lr = *reinterpret_cast<const f32x4*>(lcol + 4 * ra);
-    const f32x4 lc = *reinterpret_cast<const f32x4*>(lcol + 4 * cb);
-    const f32x4 yc = *reinterpret_cast<const f32x4*>(yrow + 4 * cb);
-    wave_sync();
+    float lr[4], lc[4], yc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      lr[u] = bperm(8 * ra + jb, lv[u]);  // L[4 ra + u][j]
+      lc[u] = bperm(8 * cb + jb, lv[u]);  // L[4 cb + u][j]
+      yc[u] = bperm(8 * jb + cb, yv[u]);  // Y[j][4 cb + u]
+    }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const float lru = 4 * ra + u > j ? lr[u] : 0.0f;
@@ -240,7 +243,7 @@ __global__ __launch_bounds__(256) void chol_inv_leaf(float* __restrict__ A, floa
   int first_bad = -1;
   auto blk = [&](float* base, int bi, int bj) { return base + bi * kLB * kLP + bj * kLB; };
   for (int kb = 0; kb < NB; ++kb) {
-    if (wave == 0) diag32(blk(sA, kb, kb), blk(sX, kb, kb), sS, lane, kb * kLB, m, first_bad);
+    if (wave == 0) diag32(blk(sA, kb, kb), blk(sX, kb, kb), lane, kb * kLB, m, first_bad);
     __syncthreads();
     // panel: L_ik = A_ik X_kk^T, one wave per block row
     {
