@@ -135,9 +135,10 @@ __device__ __forceinline__ float bperm(int src_lane, float v) {
 // row j scaled by 1 / L[j][j]; every lane fetches the pieces it needs from
 // them with ds_bpermute and applies the two rank-1 updates
 //   D[r][c] -= L[r][j] L[c][j]  (c > j),   Y[r][c] -= L[r][j] Y[j][c]  (r > j),
-// right-looking Cholesky and forward elimination fused.  (An LDS store, wave
-// barrier and load per step cost 600 cycles a column, most of the leaf.)
-
+// right-looking Cholesky and forward elimination fused.  A column step takes
+// about 600 cycles, most of the leaf; exchanging through LDS instead, or
+// blocking by 4 columns (one exchange and a rank-4 update per 4 columns, same
+// results bit for bit), measured no faster.
 __device__ __forceinline__ void diag32(float* sD, float* sXd, int lane, int col0, int lim, int& first_bad) {
   const int ra = lane >> 3, cb = lane & 7;
   float a[4][4], y[4][4];
