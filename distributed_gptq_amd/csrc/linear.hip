@@ -969,15 +969,15 @@ __global__ __launch_bounds__(64 * WAVES) void dq_split_k(LinArgs a) {
   }
 }
 
-// M <= 16, fp16 activations, 4-bit codes: the dequantised codes go straight
+// M <= 16, 4-bit codes (fp16 or bf16 activations): the dequantised codes go straight
 // from registers into the MFMA, with no LDS tile.  Lane (r, g) of a wave loads
 // codes 32 g .. 32 g + 31 of the 128-column block for weight row r (one
 // 16-byte load); at MFMA step kk it supplies the 8 codes of word kk, so step
 // kk covers columns {32 g + 8 kk + t} over the four lane groups g -- a fixed
 // bijection of the block's columns onto (step, lane group, element), which
 // the X fragments follow (lane (m, g) at step kk holds X row m at the same 8
-// columns).  Within a word the codes are decoded as pairs (t, t + 4) (an
-// AND-OR against a 1024 exponent per pair), so both operands carry their 8
+// columns).  Within a word the codes are decoded as pairs (t, t + 4) (a
+// shift and mask per pair), so both operands carry their 8
 // elements in the order 0 4 1 5 2 6 3 7 (X is permuted with v_perm).  The
 // dequantised value is (q - z) (exact) times s, rounded once, as in the LDS
 // path.  The waves of a workgroup split the blocks and sum their partial
@@ -994,7 +994,7 @@ __device__ __forceinline__ uint4 perm_0415(uint4 v) {
 }
 
 // word w (codes t = 0..7 at bits 4t) -> 4 dwords: (code t, code t + 4) for t = 0..3
-template <bool kPacked>
+template <bool kPacked, bool BF16 = false>
 __device__ __forceinline__ uint4 dq_word_0415(uint32_t w, uint32_t zz, uint32_t sh, float s, float z) {
   uint32_t p[4];
 #pragma unroll
@@ -1004,19 +1004,20 @@ __device__ __forceinline__ uint4 dq_word_0415(uint32_t w, uint32_t zz, uint32_t 
     for (int t = 0; t < 4; ++t) p[t] = dq_pair16(p[t], zz, sh);
   } else {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) p[t] = dq_pair<false>(p[t], s, z);
+    for (int t = 0; t < 4; ++t) p[t] = dq_pair<BF16>(p[t], s, z);
   }
   return uint4{p[0], p[1], p[2], p[3]};
 }
 
 // kFold (group size a multiple of 128, so a block is one group): the codes
-// enter the MFMA as the small integers q (exact in fp16, products exact in
-// fp32), and each block's 16 x 16 result is corrected per weight row as
-// s (sum q x - z sum x), with sum x from one more MFMA chain against an
-// all-ones operand.  This is the per-group zero folding of the reference's
-// fused kernels; it skips the per-weight subtract, multiply and fp16
-// rounding of the dequantised weight.
-template <int NT, int WAVES, bool kFold>
+// enter the MFMA as small integers (fp16: q, from 1024 + q less 1024; bf16:
+// 128 + q straight from the OR, exact in bf16), products are exact in fp32,
+// and each block's 16 x 16 result is corrected per weight row as
+// s (sum q' x - z' sum x) with z' = z (fp16) or z + 128 (bf16), sum x from
+// one more MFMA chain against an all-ones operand.  This is the per-group
+// zero folding of the reference's fused kernels; it skips the per-weight
+// subtract, multiply and rounding of the dequantised weight.
+template <int NT, int WAVES, bool kFold, bool BF16>
 __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
   constexpr int BN = NT / 16;
   __shared__ float red[WAVES][BN][4][64];
@@ -1057,14 +1058,21 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) xb[kk] = xok ? perm_0415(L.x[kk]) : uint4{0u, 0u, 0u, 0u};
     const int g = (b * 128 + 32 * g4) / a.gs;  // 32-bit division (K < 2^31)
+    auto mfma = [](uint4 fa, uint4 fb, f32x4 c) {
+      if constexpr (BF16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, fa), __builtin_bit_cast(bf16x8, fb),
+                                                       c, 0, 0, 0);
+      else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, fa), __builtin_bit_cast(f16x8, fb), c,
+                                                      0, 0, 0);
+    };
     if constexpr (kFold) {
       f32x4 sx = f32x4{0.f, 0.f, 0.f, 0.f};
-      const uint4 ones = uint4{0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};
+      constexpr uint32_t kOne = BF16 ? 0x3f803f80u : 0x3c003c00u;
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-        sx = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ones), __builtin_bit_cast(f16x8, xb[kk]),
-                                                    sx, 0, 0, 0);
+      for (int kk = 0; kk < 4; ++kk) sx = mfma(uint4{kOne, kOne, kOne, kOne}, xb[kk], sx);
       const f16x2 magic = __builtin_bit_cast(f16x2, 0x64006400u);
+      constexpr float kZoff = BF16 ? 128.0f : 0.0f;
 #pragma unroll
       for (int i = 0; i < BN; ++i) {
         const uint32_t w[4] = {L.cw[i].x, L.cw[i].y, L.cw[i].z, L.cw[i].w};
@@ -1073,16 +1081,19 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
         for (int kk = 0; kk < 4; ++kk) {
           uint32_t q[4];
 #pragma unroll
-          for (int u = 0; u < 4; ++u)
-            q[u] = __builtin_bit_cast(uint32_t,
-                                      __builtin_bit_cast(f16x2, ((w[kk] >> (4 * u)) & 0x000F000Fu) | 0x64006400u) - magic);
-          t = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, uint4{q[0], q[1], q[2], q[3]}),
-                                                     __builtin_bit_cast(f16x8, xb[kk]), t, 0, 0, 0);
+          for (int u = 0; u < 4; ++u) {
+            if constexpr (BF16)
+              q[u] = ((w[kk] >> (4 * u)) & 0x000F000Fu) | 0x43004300u;  // 128 + q
+            else
+              q[u] = __builtin_bit_cast(
+                  uint32_t, __builtin_bit_cast(f16x2, ((w[kk] >> (4 * u)) & 0x000F000Fu) | 0x64006400u) - magic);
+          }
+          t = mfma(uint4{q[0], q[1], q[2], q[3]}, xb[kk], t);
         }
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const float2 p = sz[(16 * i + 4 * g4 + v) * ng + g];
-          acc[i][v] = fmaf(p.x, fmaf(-p.y, sx[v], t[v]), acc[i][v]);
+          acc[i][v] = fmaf(p.x, fmaf(-(p.y + kZoff), sx[v], t[v]), acc[i][v]);
         }
       }
       return;
@@ -1093,8 +1104,8 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
       const float s = p.x, z = p.y;
       const uint32_t w[4] = {L.cw[i].x, L.cw[i].y, L.cw[i].z, L.cw[i].w};
       uint4 fa[4];
-      // GPTQ zero points are integers: the packed path, chosen for the whole wave
-      if (__all(z == rintf(z) && z >= 0.0f && z <= 1023.0f)) {
+      // GPTQ zero points are integers: the packed path (fp16), chosen for the whole wave
+      if (!BF16 && __all(z == rintf(z) && z >= 0.0f && z <= 1023.0f)) {
         const uint32_t zz = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(1024.0f + z),
                                                                 static_cast<_Float16>(1024.0f + z)});
         const uint32_t sh = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(s), static_cast<_Float16>(s)});
@@ -1102,12 +1113,10 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
         for (int kk = 0; kk < 4; ++kk) fa[kk] = dq_word_0415<true>(w[kk], zz, sh, s, z);
       } else {
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) fa[kk] = dq_word_0415<false>(w[kk], 0u, 0u, s, z);
+        for (int kk = 0; kk < 4; ++kk) fa[kk] = dq_word_0415<false, BF16>(w[kk], 0u, 0u, s, z);
       }
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, fa[kk]),
-                                                        __builtin_bit_cast(f16x8, xb[kk]), acc[i], 0, 0, 0);
+      for (int kk = 0; kk < 4; ++kk) acc[i] = mfma(fa[kk], xb[kk], acc[i]);
     }
   };
 
@@ -1159,7 +1168,7 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
   }
 }
 
-template <int NT, int WAVES>
+template <int NT, int WAVES, bool BF16>
 int launch_reg4(hipStream_t st, const LinArgs& a) {
   const size_t lds = static_cast<size_t>(NT) * a.ngroups * sizeof(float2);
   // static partial-tile buffer + the staged scales and zeros within the CU's LDS
@@ -1167,9 +1176,9 @@ int launch_reg4(hipStream_t st, const LinArgs& a) {
                "dq_reg4: %lld groups per row exceed the LDS budget", static_cast<long long>(a.ngroups));
   const dim3 grid(static_cast<unsigned>(cdiv(a.N, NT)));
   if (a.gs % 128 == 0)
-    hipLaunchKernelGGL((dq_reg4_k<NT, WAVES, true>), grid, dim3(64 * WAVES), lds, st, a);
+    hipLaunchKernelGGL((dq_reg4_k<NT, WAVES, true, BF16>), grid, dim3(64 * WAVES), lds, st, a);
   else
-    hipLaunchKernelGGL((dq_reg4_k<NT, WAVES, false>), grid, dim3(64 * WAVES), lds, st, a);
+    hipLaunchKernelGGL((dq_reg4_k<NT, WAVES, false, BF16>), grid, dim3(64 * WAVES), lds, st, a);
   return check_launch("dq_reg4");
 }
 
@@ -1353,13 +1362,13 @@ int launch_split(hipStream_t st, const LinArgs& a) {
 // 64-row tiles when there are >= 128, else split-K
 template <int BITS, bool BF16>
 int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
-  if constexpr (BITS == 4 && !BF16) {
+  if constexpr (BITS == 4) {
     // the register path stages the workgroup's scales and zeros in <= 64 KB of LDS
     if (a.M <= 16 && 64 * a.ngroups * sizeof(float2) <= 64 * 1024) {
       // measured best per shape class (28672 x 4096, 14336 x 4096, 4096 x 14336)
-      if (a.N >= 64 * 256) return launch_reg4<64, 4>(st, a);
-      if (a.N >= 32 * 256) return launch_reg4<64, 8>(st, a);
-      return launch_reg4<16, 8>(st, a);
+      if (a.N >= 64 * 256) return launch_reg4<64, 4, BF16>(st, a);
+      if (a.N >= 32 * 256) return launch_reg4<64, 8, BF16>(st, a);
+      return launch_reg4<16, 8, BF16>(st, a);
     }
   }
   if (a.M <= 16) {
@@ -1465,7 +1474,10 @@ int launch_fast(hipStream_t st, const LinArgs& a) {
       a.N * a.ngroups * 2 <= INT32_MAX && (reinterpret_cast<uintptr_t>(a.x) % 16) == 0) {
     return launch_m1_sz<BITS, BF16>(st, a);
   }
-  if (a.M <= 4) {
+  // M = 2..4: the MFMA kernels below (measured 2-3x faster than gemv_k at
+  // 28672 x 4096); gemv_k serves the layouts they do not take
+  const bool dq_layout = a.K % 128 == 0 && a.gs % 32 == 0;
+  if (a.M <= 4 && !dq_layout) {
     const size_t lds = static_cast<size_t>(a.M) * a.K * 2 + static_cast<size_t>(a.M) * nch * 4;
     if (lds <= 64 * 1024) {
       const int64_t nbatches = cdiv(a.N, kRB);
@@ -1480,7 +1492,7 @@ int launch_fast(hipStream_t st, const LinArgs& a) {
     }
   }
   // 128-column blocks, one group per 32-code chunk
-  if (a.K % 128 == 0 && a.gs % 32 == 0) return launch_dq_gemm<BITS, BF16>(st, a);
+  if (dq_layout) return launch_dq_gemm<BITS, BF16>(st, a);
   const dim3 grid(static_cast<unsigned>(cdiv(a.N, 16)), static_cast<unsigned>(cdiv(a.M, kMT * 16)));
   hipLaunchKernelGGL((dq_mfma_k<BITS, BF16>), grid, dim3(256), 0, st, a);
   return check_launch("dq_mfma");
