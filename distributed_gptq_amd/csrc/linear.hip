@@ -969,7 +969,7 @@ __global__ __launch_bounds__(64 * WAVES) void dq_split_k(LinArgs a) {
   }
 }
 
-// M <= 16, 4-bit codes (fp16 or bf16 activations): the dequantised codes go straight
+// M <= 16, 4- or 3-bit codes (fp16 or bf16 activations): the dequantised codes go straight
 // from registers into the MFMA, with no LDS tile.  Lane (r, g) of a wave loads
 // codes 32 g .. 32 g + 31 of the 128-column block for weight row r (one
 // 16-byte load); at MFMA step kk it supplies the 8 codes of word kk, so step
@@ -982,23 +982,37 @@ __global__ __launch_bounds__(64 * WAVES) void dq_split_k(LinArgs a) {
 // dequantised value is (q - z) (exact) times s, rounded once, as in the LDS
 // path.  The waves of a workgroup split the blocks and sum their partial
 // tiles in wave order.
-template <int NT>
+template <int NT, int BITS>
 struct DrBlock {
-  uint4 cw[NT / 16];
+  uint32_t cw[NT / 16][BITS];  // a lane's 32 codes of each row block
   uint4 x[4];
 };
+
+// the code pairs (8 kk + t, 8 kk + t + 4), t = 0..3, of MFMA step kk from a
+// lane's 32 codes (4-bit: word kk; 3-bit: the 24 bits at 24 kk of 3 words)
+template <int BITS>
+__device__ __forceinline__ void step_pairs(const uint32_t (&cw)[BITS], int kk, uint32_t (&p)[4]) {
+  if constexpr (BITS == 4) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) p[t] = (cw[kk] >> (4 * t)) & 0x000F000Fu;
+  } else {
+    const uint32_t v = kk == 0 ? cw[0]
+                     : kk == 1 ? __builtin_amdgcn_alignbit(cw[1], cw[0], 24)
+                     : kk == 2 ? __builtin_amdgcn_alignbit(cw[2], cw[1], 16)
+                               : cw[2] >> 8;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) p[t] = ((v >> (3 * t)) & 7u) | (((v >> (3 * t + 12)) & 7u) << 16);
+  }
+}
 
 __device__ __forceinline__ uint4 perm_0415(uint4 v) {
   return uint4{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
                __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
 }
 
-// word w (codes t = 0..7 at bits 4t) -> 4 dwords: (code t, code t + 4) for t = 0..3
+// the code pairs of a step -> 4 dwords of dequantised (code t, code t + 4)
 template <bool kPacked, bool BF16 = false>
-__device__ __forceinline__ uint4 dq_word_0415(uint32_t w, uint32_t zz, uint32_t sh, float s, float z) {
-  uint32_t p[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) p[t] = (w >> (4 * t)) & 0x000F000Fu;
+__device__ __forceinline__ uint4 dq_word_0415(uint32_t (&p)[4], uint32_t zz, uint32_t sh, float s, float z) {
   if constexpr (kPacked) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) p[t] = dq_pair16(p[t], zz, sh);
@@ -1017,7 +1031,7 @@ __device__ __forceinline__ uint4 dq_word_0415(uint32_t w, uint32_t zz, uint32_t 
 // one more MFMA chain against an all-ones operand.  This is the per-group
 // zero folding of the reference's fused kernels; it skips the per-weight
 // subtract, multiply and rounding of the dequantised weight.
-template <int NT, int WAVES, bool kFold, bool BF16>
+template <int BITS, int NT, int WAVES, bool kFold, bool BF16>
 __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
   constexpr int BN = NT / 16;
   __shared__ float red[WAVES][BN][4][64];
@@ -1041,10 +1055,18 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
   const bool xok = r16 < a.M;
   const uint16_t* xrow = a.x + (xok ? r16 : 0) * a.K;
 
-  auto load = [&](int b, DrBlock<NT>& L) {
+  auto load = [&](int b, DrBlock<NT, BITS>& L) {
     const int64_t k = static_cast<int64_t>(b) * 128 + 32 * g4;
 #pragma unroll
-    for (int i = 0; i < BN; ++i) L.cw[i] = *reinterpret_cast<const uint4*>(wrow[i] + k / 2);
+    for (int i = 0; i < BN; ++i) {
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(wrow[i] + k * BITS / 8);
+      if constexpr (BITS == 4) {
+        const uint4 v = *reinterpret_cast<const uint4*>(src);
+        L.cw[i][0] = v.x; L.cw[i][1] = v.y; L.cw[i][2] = v.z; L.cw[i][3] = v.w;
+      } else {
+        L.cw[i][0] = src[0]; L.cw[i][1] = src[1]; L.cw[i][2] = src[2];
+      }
+    }
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) L.x[kk] = *reinterpret_cast<const uint4*>(xrow + k + 8 * kk);
   };
@@ -1053,7 +1075,7 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
 #pragma unroll
   for (int i = 0; i < BN; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto block = [&](int b, const DrBlock<NT>& L) {
+  auto block = [&](int b, const DrBlock<NT, BITS>& L) {
     uint4 xb[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) xb[kk] = xok ? perm_0415(L.x[kk]) : uint4{0u, 0u, 0u, 0u};
@@ -1075,18 +1097,17 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
       constexpr float kZoff = BF16 ? 128.0f : 0.0f;
 #pragma unroll
       for (int i = 0; i < BN; ++i) {
-        const uint32_t w[4] = {L.cw[i].x, L.cw[i].y, L.cw[i].z, L.cw[i].w};
         f32x4 t = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
           uint32_t q[4];
+          step_pairs<BITS>(L.cw[i], kk, q);
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             if constexpr (BF16)
-              q[u] = ((w[kk] >> (4 * u)) & 0x000F000Fu) | 0x43004300u;  // 128 + q
+              q[u] |= 0x43004300u;  // 128 + q
             else
-              q[u] = __builtin_bit_cast(
-                  uint32_t, __builtin_bit_cast(f16x2, ((w[kk] >> (4 * u)) & 0x000F000Fu) | 0x64006400u) - magic);
+              q[u] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, q[u] | 0x64006400u) - magic);
           }
           t = mfma(uint4{q[0], q[1], q[2], q[3]}, xb[kk], t);
         }
@@ -1102,18 +1123,20 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
     for (int i = 0; i < BN; ++i) {
       const float2 p = sz[(16 * i + r16) * ng + g];
       const float s = p.x, z = p.y;
-      const uint32_t w[4] = {L.cw[i].x, L.cw[i].y, L.cw[i].z, L.cw[i].w};
       uint4 fa[4];
+      uint32_t pr[4][4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) step_pairs<BITS>(L.cw[i], kk, pr[kk]);
       // GPTQ zero points are integers: the packed path (fp16), chosen for the whole wave
       if (!BF16 && __all(z == rintf(z) && z >= 0.0f && z <= 1023.0f)) {
         const uint32_t zz = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(1024.0f + z),
                                                                 static_cast<_Float16>(1024.0f + z)});
         const uint32_t sh = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(s), static_cast<_Float16>(s)});
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) fa[kk] = dq_word_0415<true>(w[kk], zz, sh, s, z);
+        for (int kk = 0; kk < 4; ++kk) fa[kk] = dq_word_0415<true>(pr[kk], zz, sh, s, z);
       } else {
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) fa[kk] = dq_word_0415<false, BF16>(w[kk], 0u, 0u, s, z);
+        for (int kk = 0; kk < 4; ++kk) fa[kk] = dq_word_0415<false, BF16>(pr[kk], 0u, 0u, s, z);
       }
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) acc[i] = mfma(fa[kk], xb[kk], acc[i]);
@@ -1122,7 +1145,7 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
 
   // blocks b = wave, wave + WAVES, ...: two in flight; the first two are
   // issued before the scales and zeros are staged
-  DrBlock<NT> A, B;
+  DrBlock<NT, BITS> A, B;
   int b = wave;
   if (b < nblk) load(b, A);
   if (b + WAVES < nblk) load(b + WAVES, B);
@@ -1168,7 +1191,7 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
   }
 }
 
-template <int NT, int WAVES, bool BF16>
+template <int BITS, int NT, int WAVES, bool BF16>
 int launch_reg4(hipStream_t st, const LinArgs& a) {
   const size_t lds = static_cast<size_t>(NT) * a.ngroups * sizeof(float2);
   // static partial-tile buffer + the staged scales and zeros within the CU's LDS
@@ -1176,9 +1199,9 @@ int launch_reg4(hipStream_t st, const LinArgs& a) {
                "dq_reg4: %lld groups per row exceed the LDS budget", static_cast<long long>(a.ngroups));
   const dim3 grid(static_cast<unsigned>(cdiv(a.N, NT)));
   if (a.gs % 128 == 0)
-    hipLaunchKernelGGL((dq_reg4_k<NT, WAVES, true, BF16>), grid, dim3(64 * WAVES), lds, st, a);
+    hipLaunchKernelGGL((dq_reg4_k<BITS, NT, WAVES, true, BF16>), grid, dim3(64 * WAVES), lds, st, a);
   else
-    hipLaunchKernelGGL((dq_reg4_k<NT, WAVES, false, BF16>), grid, dim3(64 * WAVES), lds, st, a);
+    hipLaunchKernelGGL((dq_reg4_k<BITS, NT, WAVES, false, BF16>), grid, dim3(64 * WAVES), lds, st, a);
   return check_launch("dq_reg4");
 }
 
@@ -1362,13 +1385,14 @@ int launch_split(hipStream_t st, const LinArgs& a) {
 // 64-row tiles when there are >= 128, else split-K
 template <int BITS, bool BF16>
 int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
-  if constexpr (BITS == 4) {
-    // the register path stages the workgroup's scales and zeros in <= 64 KB of LDS
-    if (a.M <= 16 && 64 * a.ngroups * sizeof(float2) <= 64 * 1024) {
+  if constexpr (BITS == 4 || BITS == 3) {
+    // the register path stages the workgroup's scales and zeros in <= 64 KB of
+    // LDS; 3-bit rows are read as dwords (the pitch must keep them aligned)
+    if (a.M <= 16 && 64 * a.ngroups * sizeof(float2) <= 64 * 1024 && (BITS == 4 || a.pitch % 4 == 0)) {
       // measured best per shape class (28672 x 4096, 14336 x 4096, 4096 x 14336)
-      if (a.N >= 64 * 256) return launch_reg4<64, 4, BF16>(st, a);
-      if (a.N >= 32 * 256) return launch_reg4<64, 8, BF16>(st, a);
-      return launch_reg4<16, 8, BF16>(st, a);
+      if (a.N >= 64 * 256) return launch_reg4<BITS, 64, 4, BF16>(st, a);
+      if (a.N >= 32 * 256) return launch_reg4<BITS, 64, 8, BF16>(st, a);
+      return launch_reg4<BITS, 16, 8, BF16>(st, a);
     }
   }
   if (a.M <= 16) {
