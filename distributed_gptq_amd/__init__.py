@@ -5,7 +5,8 @@ Compute runs in libgptq_hip.so (hand-written gfx950 HIP kernels behind a
 C ABI, include/gptq_hip.h); this package mirrors the reference's import
 paths: ``core.gptq`` (GPTQ), ``core.quantizer`` (QuantizationConfig,
 Quantizer), ``core.dequantizer``, ``models.layers`` (QuantizedLinear and the
-gptq::linear operator) and ``kernels``.
+gptq::linear operator) and ``kernels``; ``core.checkpoint`` holds the
+reference quantizer's save/load (safetensors + JSON sidecar).
 """
 from .core.gptq import GPTQ, GPTQMultiGPU, quantize_layer_gptq
 from .core.quantizer import QuantizationConfig, Quantizer
@@ -14,7 +15,7 @@ from .core.dequantizer import GPTQDequantizer
 __version__ = "0.1.0"
 
 __all__ = ["GPTQ", "GPTQMultiGPU", "quantize_layer_gptq", "QuantizationConfig", "Quantizer", "GPTQDequantizer",
-           "QuantizedLinear", "replace_with_quantized_layers"]
+           "QuantizedLinear", "replace_with_quantized_layers", "save_quantized_model", "load_quantized_model"]
 
 
 def __getattr__(name):
@@ -22,4 +23,7 @@ def __getattr__(name):
     if name in ("QuantizedLinear", "replace_with_quantized_layers"):
         from .models import layers
         return getattr(layers, name)
+    if name in ("save_quantized_model", "load_quantized_model"):
+        from .core import checkpoint
+        return getattr(checkpoint, name)
     raise AttributeError(name)
