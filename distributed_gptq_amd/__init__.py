@@ -9,12 +9,13 @@ gptq::linear operator) and ``kernels``; ``core.checkpoint`` holds the
 reference quantizer's save/load (safetensors + JSON sidecar).
 """
 from .core.gptq import GPTQ, GPTQMultiGPU, quantize_layer_gptq
-from .core.quantizer import QuantizationConfig, Quantizer
+from .core.quantizer import DistributedGPTQuantizer, QuantizationConfig, Quantizer, quantize_model_simple
 from .core.dequantizer import GPTQDequantizer
 
 __version__ = "0.1.0"
 
-__all__ = ["GPTQ", "GPTQMultiGPU", "quantize_layer_gptq", "QuantizationConfig", "Quantizer", "GPTQDequantizer",
+__all__ = ["GPTQ", "GPTQMultiGPU", "quantize_layer_gptq", "DistributedGPTQuantizer", "QuantizationConfig", "Quantizer",
+           "quantize_model_simple", "GPTQDequantizer",
            "QuantizedLinear", "replace_with_quantized_layers", "save_quantized_model", "load_quantized_model"]
 
 

@@ -1,7 +1,8 @@
 """core: GPTQ, QuantizationConfig, Quantizer, GPTQDequantizer
 (src/distributed_gptq/core/__init__.py:5-15)."""
 from .gptq import GPTQ, GPTQMultiGPU, quantize_layer_gptq
-from .quantizer import QuantizationConfig, Quantizer
+from .quantizer import DistributedGPTQuantizer, QuantizationConfig, Quantizer, quantize_model_simple
 from .dequantizer import GPTQDequantizer
 
-__all__ = ["GPTQ", "GPTQMultiGPU", "quantize_layer_gptq", "QuantizationConfig", "Quantizer", "GPTQDequantizer"]
+__all__ = ["GPTQ", "GPTQMultiGPU", "quantize_layer_gptq", "DistributedGPTQuantizer", "QuantizationConfig", "Quantizer",
+           "quantize_model_simple", "GPTQDequantizer"]

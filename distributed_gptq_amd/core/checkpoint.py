@@ -15,7 +15,9 @@ holding QuantizedLinear modules.  The reference loads with a strict
 ``load_state_dict`` (:319-320), which needs every quantized layer of ``model``
 to be a QuantizedLinear of the right shape already; here each name in
 ``quantized_layers`` that is still an ``nn.Linear`` is first replaced by a
-QuantizedLinear whose buffers take the saved shapes and dtypes. A file without
+QuantizedLinear whose buffers take the saved shapes and dtypes. Quantized
+layers saved as ``nn.Linear`` (dequantized weights, the reference's in-place
+result) have no ``layers`` entry and load as they are. A file without
 ``layers`` (the reference's own) is read by inferring the layout from the
 buffer shapes and ``quantization_config.bits``.
 
@@ -85,14 +87,16 @@ def save_quantized_model(model: nn.Module, save_path: Union[str, Path], save_for
     save_path.parent.mkdir(parents=True, exist_ok=True)
     qmods = _quantized_modules(model)
     names = list(quantized_layers) if quantized_layers is not None else list(qmods)
-    missing = [n for n in names if n not in qmods]
-    if missing:
-        raise ValueError(f"not QuantizedLinear modules of the model: {missing}")
+    mods = dict(model.named_modules())
+    bad = [n for n in names if not isinstance(mods.get(n), (QuantizedLinear, nn.Linear))]
+    if bad:
+        raise ValueError(f"neither QuantizedLinear nor nn.Linear modules of the model: {bad}")
     meta = {
         "quantization_config": _config_dict(quant_config, qmods),
         "quantized_layers": names,
         "quantization_errors": {k: float(v) for k, v in (quantization_errors or {}).items()},
-        "layers": {n: _layer_info(qmods[n]) for n in names},
+        # layers kept as nn.Linear (holding dequantized weights) need no layout
+        "layers": {n: _layer_info(qmods[n]) for n in names if n in qmods},
     }
     state = _cpu_state(model)
     if save_format == "safetensors":
@@ -198,6 +202,8 @@ def load_quantized_model(model: nn.Module, load_path: Union[str, Path], load_for
     config = QuantizationConfig(**meta["quantization_config"])
     layers = meta.get("layers") or {}
     for name in meta["quantized_layers"]:
+        if name not in layers and f"{name}.qweight" not in state and f"{name}.weight" in state:
+            continue  # an nn.Linear holding dequantized weights: loaded as it is
         info = layers.get(name) or _infer_info(name, state, config)
         _check_buffers(name, info, state)
         _install(model, name, info, state)

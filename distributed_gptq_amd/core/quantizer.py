@@ -12,13 +12,18 @@ arithmetic runs in the HIP library.
 """
 from __future__ import annotations
 
+import logging
+import time
 from dataclasses import asdict, dataclass
+from typing import Any, Callable, Dict, List, Optional, Tuple, Union
 
 import torch
 import torch.nn as nn
 
 from .. import _lib as L
 from .. import _ops
+
+logger = logging.getLogger(__name__)
 
 
 @dataclass
@@ -135,3 +140,335 @@ class Quantizer(nn.Module):
 
     def ready(self):
         return bool(torch.all(self.scale != 0))
+
+
+# ------------------------------------------------------------- driver --
+
+class _HookError(RuntimeError):
+    """A failure inside the Hessian hooks (never skipped like a failing
+    calibration batch)."""
+
+
+class _SharedHessians:
+    """Hessians of a calibration pass, one per group of layers that received
+    the same input tensor in every batch so far (q/k/v, gate/up).
+
+    Every layer starts alone.  A layer with no samples yet joins a group
+    that also had none before this batch and was just given the same tensor
+    (both Hessians are then that tensor's X^T X).  A group of several layers
+    adds its input once every member has seen the batch: members whose input
+    differs from the first member's leave the group with a copy of the
+    group's Hessian as it was before this batch (exact: nothing of this batch
+    has been added yet), and each distinct input is added once.  Inputs are
+    compared by storage, offset, shape, stride, dtype and version counter;
+    a group's pending inputs are kept referenced (so a reused allocation
+    cannot pass for the same input) and cloned (so an in-place change after
+    the first member's call is seen as a different input, not lost).  With
+    ``share=False`` every layer keeps its own Hessian."""
+
+    def __init__(self, layers: Dict[str, nn.Linear], device: torch.device, share: bool, make_acc=None):
+        if make_acc is None:
+            from .gptq import GPTQ
+
+            def make_acc(layer):
+                return GPTQ(layer, device=device, token_buffer=0)
+        # make_acc(layer) -> an object with add_batch(x), the H property,
+        # nsamples and free(): the GPTQ class, or a stand-in in tests
+        self._make_acc = make_acc
+        self.layers, self.device, self.share = layers, device, share
+        self.group_of: Dict[str, int] = {}
+        self.members: Dict[int, List[str]] = {}
+        self.acc: Dict[int, Any] = {}
+        for name in layers:
+            self._new_group([name], None)
+        # this batch: group -> {key: (input, clone, members)} still to settle,
+        # and key -> (group, input) for groups that had no samples before it
+        self.pending: Dict[int, Dict[tuple, Tuple[torch.Tensor, torch.Tensor, List[str]]]] = {}
+        self.fresh: Dict[tuple, Tuple[int, torch.Tensor]] = {}
+
+    def _new_group(self, names: List[str], copy_from) -> int:
+        gid = len(self.acc)
+        q = self._make_acc(self.layers[names[0]])
+        if copy_from is not None and copy_from.nsamples:
+            q.H = copy_from.H.clone()
+            q.nsamples = copy_from.nsamples
+        self.acc[gid], self.members[gid] = q, list(names)
+        for n in names:
+            self.group_of[n] = gid
+        return gid
+
+    @staticmethod
+    def _key(x: torch.Tensor) -> tuple:
+        return (x.untyped_storage().data_ptr(), x.storage_offset(), tuple(x.shape), tuple(x.stride()), x.dtype,
+                x._version)
+
+    def add(self, name: str, x: torch.Tensor) -> None:
+        gid = self.group_of[name]
+        key = self._key(x)
+        if len(self.members[gid]) == 1:
+            acc = self.acc[gid]
+            if self.share and acc.nsamples == 0:
+                hit = self.fresh.get(key)
+                if hit is not None and hit[0] != gid:
+                    g = hit[0]
+                    self.members[g].append(name)
+                    self.group_of[name] = g
+                    self.members[gid] = []
+                    return
+                self.fresh[key] = (gid, x)
+            acc.add_batch(x)
+            return
+        if any(name in names for _, _, names in self.pending.get(gid, {}).values()):
+            # a layer called twice in one forward: settle what the group has
+            # seen so far (members not yet called split off), then go on
+            self._settle(gid)
+            self.add(name, x)
+            return
+        part = self.pending.setdefault(gid, {})
+        if key not in part:
+            part[key] = (x, x.clone(), [])
+        part[key][2].append(name)
+        if sum(len(v[2]) for v in part.values()) == len(self.members[gid]):
+            self._settle(gid)
+
+    def _settle(self, gid: int) -> None:
+        part = list(self.pending.pop(gid).values())
+        fired = {n for _, _, names in part for n in names}
+        idle = [n for n in self.members[gid] if n not in fired]
+        acc = self.acc[gid]
+        # split before adding anything of this batch, so the copies are exact
+        moved = [(self._new_group(names, acc), xc) for _, xc, names in part[1:]]
+        if idle:
+            self._new_group(idle, acc)
+        self.members[gid] = list(part[0][2])
+        for g, xc in [(gid, part[0][1])] + moved:
+            self.acc[g].add_batch(xc)
+
+    def end_batch(self) -> None:
+        for gid in list(self.pending):
+            self._settle(gid)
+        self.fresh.clear()
+
+    def groups(self) -> Dict[int, List[str]]:
+        return {g: list(m) for g, m in self.members.items() if m}
+
+
+class DistributedGPTQuantizer:
+    """Model-level GPTQ driver (core/quantizer.py:52-356) on one GPU.
+
+    ``quantize_model`` finds the nn.Linear layers (:167-179), runs the
+    calibration forward with hooks (:194-246) and quantizes every layer with
+    canonical GPTQ (:129-151).  The reference stores every layer input on the
+    host (``.cpu()``, :210) and later runs each layer again per batch to feed
+    ``add_batch`` (distributed/coordinator.py:213-218); here the hooks feed
+    each input straight into the Hessian kernel, and layers fed the same
+    tensor share one Hessian and one factorisation (bit-identical results,
+    less work).  Layers are quantized a few Hessian groups at a time on side
+    streams (``pipeline.quantize_layers``).
+
+    With ``quantization_config.save_packed`` (the default) each quantized
+    layer is replaced by a QuantizedLinear holding its packed codes, the form
+    the W4A16/W3A16 kernels serve; otherwise the nn.Linear keeps the
+    dequantized weights.  Divergences: nn.Conv2d layers are not quantized;
+    a list of calibration tensors is iterated one tensor per batch (the
+    reference wraps it in ``TensorDataset(*data)``, :185-192, which yields
+    only the first tensor's rows); ``distributed_config`` with more than one
+    process is refused.
+    """
+
+    def __init__(self, quantization_config: Optional[QuantizationConfig] = None, distributed_config=None,
+                 device: Optional[Union[str, torch.device]] = None, share_hessians: bool = True,
+                 groups_per_step: int = 4):
+        self.quant_config = quantization_config or QuantizationConfig()
+        self.quant_config.validate()
+        world = getattr(distributed_config, "world_size", 1) if distributed_config is not None else 1
+        if world > 1:
+            raise NotImplementedError("this build quantizes on one GPU per process (world_size must be 1)")
+        self.dist_config = distributed_config
+        self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device()
+                                                                                  if torch.cuda.is_available() else 0)
+        self.share_hessians = share_hessians
+        self.groups_per_step = max(1, int(groups_per_step))
+        self.quantized_layers: Dict[str, Dict[str, Any]] = {}
+        self.quantization_errors: Dict[str, float] = {}
+
+    @property
+    def config(self) -> QuantizationConfig:
+        return self.quant_config
+
+    # ------------------------------------------------------------ layers --
+    def _find_layers_to_quantize(self, model: nn.Module) -> Dict[str, nn.Linear]:
+        """nn.Linear layers with more than 1000 weights (:167-179)."""
+        return {n: m for n, m in model.named_modules() if isinstance(m, nn.Linear) and m.weight.numel() > 1000}
+
+    def _get_quantizable_layers(self, model: nn.Module) -> List[Tuple[str, nn.Linear]]:
+        return list(self._find_layers_to_quantize(model).items())
+
+    def _resolve_layers(self, model, layers_to_quantize) -> Dict[str, nn.Linear]:
+        if layers_to_quantize is None:
+            return self._find_layers_to_quantize(model)
+        mods = dict(model.named_modules())
+        if isinstance(layers_to_quantize, dict):
+            layers = dict(layers_to_quantize)
+        else:
+            missing = [n for n in layers_to_quantize if n not in mods]
+            if missing:
+                raise ValueError(f"no such modules in the model: {missing}")
+            layers = {n: mods[n] for n in layers_to_quantize}
+        bad = [n for n, m in layers.items() if not isinstance(m, nn.Linear)]
+        if bad:
+            raise NotImplementedError(f"only nn.Linear layers are quantized here, not {bad}")
+        return layers
+
+    # ------------------------------------------------------- calibration --
+    @staticmethod
+    def _inputs(batch):
+        if isinstance(batch, (list, tuple)):
+            batch = batch[0]
+        return batch
+
+    @torch.no_grad()
+    def _collect_hessians(self, model: nn.Module, calibration_data, layers: Dict[str, nn.Linear]) -> _SharedHessians:
+        """Calibration forward (:194-246) with the Hessians accumulated in the
+        hooks; stops once ``calibration_samples`` rows have been seen."""
+        hs = _SharedHessians(layers, self.device, self.share_hessians)
+
+        def hook_for(name):
+            def hook(module, inp, out):
+                x = inp[0] if isinstance(inp, tuple) else inp
+                try:
+                    hs.add(name, x.detach())
+                except Exception as e:
+                    raise _HookError(f"Hessian accumulation for {name}: {e}") from e
+            return hook
+
+        handles = [m.register_forward_hook(hook_for(n)) for n, m in layers.items()]
+        seen = ok = 0
+        try:
+            for batch in calibration_data:
+                if seen >= self.quant_config.calibration_samples:
+                    break
+                b = self._inputs(batch)
+                try:
+                    if isinstance(b, dict):
+                        b = {k: v.to(self.device) if torch.is_tensor(v) else v for k, v in b.items()}
+                        rows = next(v for v in b.values() if torch.is_tensor(v)).shape[0]
+                        model(**b)
+                    else:
+                        b = b.to(self.device)
+                        rows = b.shape[0]
+                        model(b)
+                    ok += 1
+                except _HookError:
+                    raise
+                except Exception as e:  # the reference skips a failing batch (:232-236)
+                    logger.warning("error during calibration forward, batch skipped: %s", e)
+                    rows = 0
+                finally:
+                    hs.end_batch()
+                seen += rows
+        finally:
+            for h in handles:
+                h.remove()
+        if ok == 0:
+            raise ValueError("no calibration batch ran through the model")
+        return hs
+
+    # ---------------------------------------------------------- quantize --
+    def quantize_model(self, model: nn.Module, calibration_data, layers_to_quantize=None,
+                       save_path: Optional[str] = None, progress_callback: Optional[Callable] = None) -> nn.Module:
+        """core/quantizer.py:79-165: calibrate, quantize every layer, optionally
+        save.  ``progress_callback(done, total, name, stats)`` after each
+        layer."""
+        from .. import pipeline
+        from ..models.layers import QuantizedLinear
+        L.require_gpu()
+        t0 = time.time()
+        model.eval()
+        layers = self._resolve_layers(model, layers_to_quantize)
+        if not layers:
+            return model
+        for n, m in layers.items():
+            if m.weight.device.type != "cuda":
+                raise ValueError(f"layer {n} is on {m.weight.device}; move the model to the GPU first")
+        cfg = self.quant_config
+        logger.info("found %d layers to quantize", len(layers))
+        hs = self._collect_hessians(model, calibration_data, layers)
+        groups = hs.groups()
+        for g, names in groups.items():
+            if hs.acc[g].nsamples == 0:
+                raise ValueError(f"layers {names} received no calibration input")
+        # largest Hessians first; a few groups per step bound the memory held
+        # by results
+        order = sorted(groups, key=lambda g: -layers[groups[g][0]].in_features)
+        parents = {n: m for n, m in model.named_modules()}
+        total, done = len(layers), 0
+        for i in range(0, len(order), self.groups_per_step):
+            step = order[i:i + self.groups_per_step]
+            weights = {n: layers[n].weight.data for g in step for n in groups[g]}
+            hkeys = {n: str(g) for g in step for n in groups[g]}
+            hess = {str(g): (hs.acc[g].H, hs.acc[g].nsamples) for g in step}
+            res = pipeline.quantize_layers(weights, hkeys, hess, bits=cfg.bits, group_size=cfg.group_size,
+                                           blocksize=cfg.blocksize, percdamp=cfg.percdamp, actorder=cfg.actorder,
+                                           want_dequant=not cfg.save_packed)
+            for g in step:
+                hs.acc[g].free()
+            for g in step:
+                for n in groups[g]:
+                    r, lin = res[n], layers[n]
+                    if cfg.save_packed:
+                        K = lin.in_features
+                        gs = K if cfg.group_size <= 0 or cfg.group_size > K else cfg.group_size
+                        q = QuantizedLinear(cfg.bits, gs, K, lin.out_features, bias=lin.bias is not None,
+                                            packed=True).to(lin.weight.device)
+                        q.pack_weights(r.codes, r.scale, r.zero, r.g_idx)
+                        if lin.bias is not None:
+                            q.bias.data = lin.bias.data.clone()
+                        parent_name, _, attr = n.rpartition(".")
+                        setattr(parents[parent_name] if parent_name else model, attr, q)
+                    else:
+                        lin.weight.data.copy_(r.dequant)
+                    err = float(r.losses_sum)
+                    stats = {"total_error": err, "bits": cfg.bits, "group_size": cfg.group_size,
+                             "nsamples": hs.acc[g].nsamples, "hessian_shared_with": [m for m in groups[g] if m != n]}
+                    self.quantized_layers[n] = stats
+                    self.quantization_errors[n] = err
+                    done += 1
+                    if progress_callback is not None:
+                        progress_callback(done, total, n, stats)
+            del res
+        self._log_quantization_summary(time.time() - t0)
+        if save_path:
+            self.save_quantized_model(model, save_path)
+        return model
+
+    def _log_quantization_summary(self, elapsed_time: float) -> None:
+        total = sum(self.quantization_errors.values())
+        n = len(self.quantization_errors)
+        logger.info("quantized %d layers in %.2f s, total error %.6g, average %.6g", n, elapsed_time, total,
+                    total / n if n else 0.0)
+
+    # ------------------------------------------------------- save / load --
+    def save_quantized_model(self, model: nn.Module, save_path: str, save_format: str = "safetensors") -> None:
+        """core/quantizer.py:248-291."""
+        from .checkpoint import save_quantized_model
+        save_quantized_model(model, save_path, save_format, quant_config=self.quant_config,
+                             quantization_errors=self.quantization_errors,
+                             quantized_layers=list(self.quantized_layers))
+
+    def load_quantized_model(self, model: nn.Module, load_path: str, load_format: str = "safetensors") -> nn.Module:
+        """core/quantizer.py:293-335: restores the config, layer list and
+        errors along with the weights."""
+        from .checkpoint import load_quantized_model
+        model, meta = load_quantized_model(model, load_path, load_format, return_metadata=True)
+        self.quant_config = meta["quant_config"]
+        self.quantized_layers = {n: {} for n in meta["quantized_layers"]}
+        self.quantization_errors = meta["quantization_errors"]
+        return model
+
+
+def quantize_model_simple(model: nn.Module, calibration_data, bits: int = 4,
+                          save_path: Optional[str] = None) -> nn.Module:
+    """core/quantizer.py:358-383."""
+    return DistributedGPTQuantizer(QuantizationConfig(bits=bits)).quantize_model(model, calibration_data,
+                                                                               save_path=save_path)

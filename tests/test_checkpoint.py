@@ -173,7 +173,7 @@ def test_errors(tmp_path):
     path = tmp_path / "m.safetensors"
     with pytest.raises(ValueError, match="save_format"):
         save_quantized_model(src, path, save_format="npz")
-    with pytest.raises(ValueError, match="not QuantizedLinear"):
+    with pytest.raises(ValueError, match="neither QuantizedLinear"):
         save_quantized_model(src, path, quantized_layers=["layers.0.norm"])
     save_quantized_model(src, path)
     with pytest.raises(ValueError, match="load_format"):
@@ -200,7 +200,7 @@ def test_errors(tmp_path):
         load_quantized_model(Renamed(), path)
     # a sidecar naming a layer whose buffers are missing
     meta = json.loads(path.with_suffix(".json").read_text())
-    meta["quantized_layers"].append("layers.1.attn.o_proj")
+    meta["quantized_layers"].append("layers.1.attn.k_proj")
     path.with_suffix(".json").write_text(json.dumps(meta))
     with pytest.raises(ValueError, match="no buffers"):
         load_quantized_model(Model(seed=2), path)

@@ -1,0 +1,309 @@
+"""The model-level driver ``DistributedGPTQuantizer`` (core/quantizer.py:52-383
+of the reference).
+
+CPU tests drive the Hessian hooks with a float64 stand-in accumulator: with
+shared Hessians every layer's Hessian and sample count must equal, bit for
+bit, what it gets when every layer accumulates alone, whatever the sharing
+pattern does (a shared input that later diverges, a layer skipped in a
+batch, a layer called twice, a shared input modified in place between two
+of its layers, a failing batch).
+
+GPU tests quantize a small two-block model end to end: each layer
+bit-identical to a per-layer GPTQ fed the same inputs, ||WX - QX||^2 within
+1% of the fp64 oracle's, shared against unshared Hessians bit-identical, and
+save/load with bit-identical outputs."""
+import functools
+import logging
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+
+class Acc:
+    """float64 stand-in for the GPTQ accumulator (add_batch, H, nsamples)."""
+
+    def __init__(self, layer):
+        self._H = None
+        self.nsamples = 0
+
+    @property
+    def H(self):
+        return self._H
+
+    @H.setter
+    def H(self, v):
+        self._H = v
+
+    def add_batch(self, x):
+        x = x.unsqueeze(0) if x.dim() == 2 else x
+        self.nsamples += x.shape[0]
+        X = x.reshape(-1, x.shape[-1]).double()
+        self._H = X.T @ X if self._H is None else self._H + X.T @ X
+
+    def free(self):
+        self._H = None
+
+
+class Block(nn.Module):
+    def __init__(self, d=64, f=96):
+        super().__init__()
+        self.norm1, self.norm2 = nn.LayerNorm(d), nn.LayerNorm(d)
+        self.q_proj, self.k_proj, self.v_proj = nn.Linear(d, d), nn.Linear(d, d // 2), nn.Linear(d, d // 2)
+        self.o_proj = nn.Linear(d, d)
+        self.gate_proj, self.up_proj = nn.Linear(d, f, bias=False), nn.Linear(d, f, bias=False)
+        self.down_proj = nn.Linear(f, d, bias=False)
+
+    def forward(self, x):
+        h = self.norm1(x)
+        q, k, v = self.q_proj(h), self.k_proj(h), self.v_proj(h)
+        a = q * torch.sigmoid(torch.cat([k, v], -1))
+        x = x + self.o_proj(a)
+        h = self.norm2(x)
+        return x + self.down_proj(F.silu(self.gate_proj(h)) * self.up_proj(h))
+
+
+class Tiny(nn.Module):
+    def __init__(self, seed=0, d=64, f=96):
+        super().__init__()
+        torch.manual_seed(seed)
+        self.layers = nn.ModuleList([Block(d, f), Block(d, f)])
+
+    def forward(self, x):
+        for b in self.layers:
+            x = b(x)
+        return x
+
+
+def _hessians(model, data, share, samples=128):
+    from distributed_gptq_amd.core import quantizer as Q
+    dq = Q.DistributedGPTQuantizer(Q.QuantizationConfig(calibration_samples=samples), device="cpu",
+                                   share_hessians=share)
+    layers = dq._find_layers_to_quantize(model)
+    orig = Q._SharedHessians
+    Q._SharedHessians = functools.partial(orig, make_acc=Acc)
+    try:
+        hs = dq._collect_hessians(model, data, layers)
+    finally:
+        Q._SharedHessians = orig
+    return hs, layers
+
+
+def _per_layer(hs, layers):
+    return {n: (hs.acc[hs.group_of[n]].H, hs.acc[hs.group_of[n]].nsamples) for n in layers}
+
+
+def _assert_exact(a, b):
+    assert set(a) == set(b)
+    for n in a:
+        assert a[n][1] == b[n][1], n
+        assert torch.equal(a[n][0], b[n][0]), n
+
+
+def test_shared_hessians_equal_separate_ones():
+    model = Tiny().eval()
+    g = torch.Generator().manual_seed(1)
+    data = [torch.randn(2, 8, 64, generator=g) for _ in range(4)]
+    hs, layers = _hessians(model, data, share=True)
+    sep, _ = _hessians(model, data, share=False)
+    _assert_exact(_per_layer(hs, layers), _per_layer(sep, layers))
+    groups = sorted(sorted(m) for m in hs.groups().values())
+    want = []
+    for i in range(2):
+        p = f"layers.{i}."
+        want += [[p + "q_proj", p + "k_proj", p + "v_proj"], [p + "o_proj"], [p + "gate_proj", p + "up_proj"],
+                 [p + "down_proj"]]
+    assert groups == sorted(sorted(w) for w in want)
+    assert all(n == 8 for _, n in _per_layer(hs, layers).values())
+
+
+class Switch(nn.Module):
+    """a and b share an input while ``mode`` is 0; later batches feed b a
+    different tensor (mode 1), skip c (mode 2), call a twice (mode 3), or
+    modify the shared input in place between a and b (mode 4)."""
+
+    def __init__(self):
+        super().__init__()
+        torch.manual_seed(3)
+        self.a, self.b, self.c = nn.Linear(40, 40), nn.Linear(40, 40), nn.Linear(40, 40)
+        self.mode = 0
+
+    def forward(self, x):
+        y = self.a(x)
+        if self.mode == 3:
+            y = y + self.a(x * 0.5)
+        if self.mode == 4:
+            x.mul_(2.0)
+        z = self.b(x if self.mode != 1 else x + 1.0)
+        if self.mode != 2:
+            z = z + self.c(x)
+        return y + z
+
+
+class Modes:
+    def __init__(self, model, x, modes):
+        self.model, self.x, self.modes = model, x, modes
+
+    def __iter__(self):
+        for i, m in enumerate(self.modes):
+            self.model.mode = m
+            yield self.x[i].clone()
+
+
+@pytest.mark.parametrize("modes", [[0, 0, 1, 0], [0, 2, 0, 0], [0, 3, 0, 1], [1, 0, 2, 3], [2, 2, 0, 0]])
+def test_sharing_splits_exactly(modes):
+    model = Switch().eval()
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(len(modes), 3, 5, 40, generator=g)
+    hs, layers = _hessians(model, Modes(model, x, modes), share=True)
+    sep, _ = _hessians(model, Modes(model, x, modes), share=False)
+    _assert_exact(_per_layer(hs, layers), _per_layer(sep, layers))
+
+
+@pytest.mark.parametrize("modes", [[0, 4], [4, 0, 4], [0, 0, 4, 1]])
+def test_in_place_change_of_a_shared_input_splits_exactly(modes):
+    model = Switch().eval()
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(len(modes), 3, 5, 40, generator=g)
+    hs, layers = _hessians(model, Modes(model, x, modes), share=True)
+    sep, _ = _hessians(model, Modes(model, x, modes), share=False)
+    _assert_exact(_per_layer(hs, layers), _per_layer(sep, layers))
+    assert hs.group_of["a"] != hs.group_of["b"]
+
+
+def test_calibration_samples_and_failing_batch(caplog):
+    model = Tiny().eval()
+    g = torch.Generator().manual_seed(5)
+    data = [torch.randn(2, 8, 64, generator=g), torch.randn(2, 8, 32, generator=g)] + \
+           [torch.randn(2, 8, 64, generator=g) for _ in range(4)]
+    with caplog.at_level(logging.WARNING):
+        hs, layers = _hessians(model, data, share=True, samples=5)
+    assert "batch skipped" in caplog.text
+    # batches run while fewer than 5 rows were seen: 2 + (failed) + 2 + 2
+    assert all(n == 6 for _, n in _per_layer(hs, layers).values())
+    with pytest.raises(ValueError, match="no calibration batch"):
+        _hessians(model, [torch.randn(1, 8, 32)], share=True)
+
+
+def test_layer_selection_and_errors():
+    from distributed_gptq_amd.core.quantizer import DistributedGPTQuantizer, QuantizationConfig
+    model = nn.Sequential(nn.Linear(10, 20), nn.ReLU(), nn.Linear(20, 5), nn.Linear(64, 64))
+    dq = DistributedGPTQuantizer(QuantizationConfig(bits=4, group_size=64), device="cpu")
+    assert dq.config.bits == 4 and dq.config.group_size == 64
+    # more than 1000 weights (core/quantizer.py:171-177)
+    assert [n for n, _ in dq._get_quantizable_layers(model)] == ["3"]
+    assert list(dq._resolve_layers(model, ["0", "2"])) == ["0", "2"]
+    with pytest.raises(ValueError, match="no such modules"):
+        dq._resolve_layers(model, ["7"])
+    with pytest.raises(NotImplementedError):
+        dq._resolve_layers(model, ["1"])
+
+    class DC:
+        world_size = 2
+
+    with pytest.raises(NotImplementedError, match="one GPU"):
+        DistributedGPTQuantizer(distributed_config=DC())
+
+
+# ------------------------------------------------------------------ GPU --
+
+def _capture(model, data):
+    """Per-layer inputs as the hooks see them (GPU clones, in call order) and
+    fp64 raw Hessians with sample counts."""
+    xs, H, ns, hooks = {}, {}, {}, []
+    for n, m in model.named_modules():
+        if isinstance(m, nn.Linear):
+            def hook(mod, inp, out, n=n):
+                xs.setdefault(n, []).append(inp[0].detach().clone())
+                x = inp[0].detach().double().cpu()
+                X = x.reshape(-1, x.shape[-1]).numpy()
+                H[n] = H.get(n, 0) + X.T @ X
+                ns[n] = ns.get(n, 0) + x.shape[0]
+            hooks.append(m.register_forward_hook(hook))
+    with torch.no_grad():
+        for b in data:
+            model(b)
+    for h in hooks:
+        h.remove()
+    return xs, H, ns
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bits,gs,actorder", [(4, 32, True), (3, 64, False)])
+def test_quantize_model_matches_per_layer_gptq(hip, tmp_path, bits, gs, actorder):
+    """Bit-exact against one GPTQ object per layer fed the same inputs in the
+    same order (the reference's coordinator loop, distributed/coordinator.py:
+    203-228, without the host round trip); ||WX - QX||^2 within 1% of the
+    fp64 oracle's.  The layer inputs are LayerNorm outputs with outlier
+    features, whose Hessians are near-singular along the all-ones direction:
+    fp32 and fp64 factorisations then flip ~0.2% of the codes, so code
+    agreement with the oracle is checked by the kernel parity tests on
+    better-conditioned inputs, not here."""
+    import copy
+
+    from oracle import gptq_oracle as O
+
+    from distributed_gptq_amd import GPTQ, DistributedGPTQuantizer, QuantizationConfig, load_quantized_model
+    from distributed_gptq_amd.models.layers import QuantizedLinear
+    base = Tiny(seed=2, d=128, f=256).cuda().half()
+    g = torch.Generator(device="cuda").manual_seed(6)
+    data = [torch.randn(2, 32, 128, device="cuda", generator=g).half() for _ in range(6)]
+    for b in data:
+        b[..., :3] *= 8
+    W0 = {n: m.weight.detach().double().cpu().numpy() for n, m in base.named_modules() if isinstance(m, nn.Linear)}
+    xs, Hn, ns = _capture(base, data)
+    calls = []
+    cfg = QuantizationConfig(bits=bits, group_size=gs, actorder=actorder)
+    model = copy.deepcopy(base)
+    dq = DistributedGPTQuantizer(cfg)
+    out = dq.quantize_model(model, data, save_path=str(tmp_path / "q.safetensors"),
+                            progress_callback=lambda *a: calls.append(a))
+    assert out is model
+    assert [c[0] for c in calls] == list(range(1, len(W0) + 1)) and calls[-1][1] == len(W0)
+    assert set(dq.quantization_errors) == set(W0)
+    ref_model = copy.deepcopy(base)
+    mods, ref_mods = dict(model.named_modules()), dict(ref_model.named_modules())
+    for n in W0:
+        q = mods[n]
+        assert isinstance(q, QuantizedLinear)
+        gq = GPTQ(ref_mods[n], bits=bits, group_size=gs, actorder=actorder, device="cuda", token_buffer=0)
+        for x in xs[n]:
+            gq.add_batch(x)
+        st = gq.fasterquant()
+        r = QuantizedLinear.from_gptq(gq)
+        for f in ("qweight", "scales", "zeros", "g_idx", "bias"):
+            a_, b_ = getattr(q, f), getattr(r, f)
+            assert (a_ is None) == (b_ is None), (n, f)
+            if a_ is not None:
+                assert a_.dtype == b_.dtype and torch.equal(a_, b_), (n, f)
+        assert dq.quantization_errors[n] == pytest.approx(st["total_error"], rel=1e-4), n
+        assert dq.quantized_layers[n]["nsamples"] == ns[n] == 12
+        ref = O.gptq_canonical(W0[n], Hn[n], ns[n], bits, gs, 128, 0.01, actorder=actorder)
+        e_gpu = O.layer_error(W0[n], q.unpack_weights().double().cpu().numpy(), Hn[n])
+        e_ref = O.layer_error(W0[n], ref["dequant"], Hn[n])
+        assert abs(e_gpu - e_ref) <= 0.01 * e_ref, (n, e_gpu, e_ref)
+    # the saved model loads into the unquantized architecture with identical outputs
+    fresh = load_quantized_model(Tiny(seed=9, d=128, f=256).cuda().half(), tmp_path / "q.safetensors")
+    x = torch.randn(3, 16, 128, device="cuda", generator=g).half()
+    with torch.no_grad():
+        assert torch.equal(model(x), fresh(x))
+
+
+@pytest.mark.gpu
+def test_shared_and_separate_hessians_bit_identical(hip):
+    import copy
+
+    from distributed_gptq_amd import DistributedGPTQuantizer, QuantizationConfig
+    base = Tiny(seed=4, d=128, f=256).cuda().half()
+    g = torch.Generator(device="cuda").manual_seed(7)
+    data = [torch.randn(2, 32, 128, device="cuda", generator=g).half() for _ in range(4)]
+    cfg = QuantizationConfig(bits=4, group_size=64, actorder=True, save_packed=False)
+    a, b = copy.deepcopy(base), copy.deepcopy(base)
+    DistributedGPTQuantizer(cfg, share_hessians=True).quantize_model(a, data)
+    DistributedGPTQuantizer(cfg, share_hessians=False, groups_per_step=1).quantize_model(b, data)
+    for (n, ma), mb in zip(a.named_modules(), b.modules()):
+        if isinstance(ma, nn.Linear):
+            assert torch.equal(ma.weight, mb.weight), n
+            assert not torch.equal(ma.weight, dict(base.named_modules())[n].weight), n
