@@ -1379,10 +1379,16 @@ int launch_split(hipStream_t st, const LinArgs& a) {
   return check_launch("dq_split");
 }
 
-// M <= 16: split-K with 16 waves, weight rows per workgroup chosen so that
-// the grid stays >= 256 workgroups while X is re-read by fewer of them;
-// M > 16: the tiled kernel with 128-row tiles when there are >= 256 of them,
-// 64-row tiles when there are >= 128, else split-K
+// M <= 16: the register path (4/3-bit) or split-K with 16 waves, weight rows
+// per workgroup chosen so that the grid stays >= 256 workgroups while X is
+// re-read by fewer of them.  M > 16 (measured on MI355X at N x K = 28672 x
+// 4096, 14336 x 4096, 4096 x 14336 and 4096 x 4096, M = 32-128): 64 x 64
+// tiles when there are >= 192 of them (128-column steps up to 512 tiles;
+// beyond, 64-column steps, where two workgroups per CU pay, on 64 x 128
+// tiles for M > 64), 128 x 128 tiles
+// for M > 128 when there are >= 256 of those; otherwise split-K over
+// 16-row workgroups (one per 16 weight rows fills the GPU at N = 4096),
+// with M tiles of 32, 64 or 128 rows.
 template <int BITS, bool BF16>
 int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
   if constexpr (BITS == 4 || BITS == 3) {
@@ -1400,22 +1406,28 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
     if (a.N >= 32 * 256) return launch_split<BITS, BF16, 32, 16, 16>(st, a);
     return launch_split<BITS, BF16, 16, 16, 16>(st, a);
   }
-  const int64_t mt = a.M <= 64 ? 64 : 128;
-  const int64_t t128 = cdiv(a.N, 128) * cdiv(a.M, mt), t64 = cdiv(a.N, 64) * cdiv(a.M, mt);
-  if (t128 >= 256 || t64 >= 128) {
-    const bool wide = t128 >= 256;
-    const dim3 grid(static_cast<unsigned>(cdiv(a.N, wide ? 128 : 64)), static_cast<unsigned>(cdiv(a.M, mt)));
-    if (wide && mt == 64) hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 128, 64, 64>), grid, dim3(256), 0, st, a);
-    else if (wide) hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 128, 128, 64>), grid, dim3(256), 0, st, a);
-    // 64-row tiles: 128-column steps while one workgroup per CU is all the grid
-    // gives; 64-column steps (half the LDS) when two fit per CU and are needed
-    else if (t64 <= 256 && mt == 64) hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 64, 64, 128>), grid, dim3(256), 0, st, a);
-    else if (t64 <= 256) hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 64, 128, 128>), grid, dim3(256), 0, st, a);
-    else if (mt == 64) hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 64, 64, 64>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 64, 128, 64>), grid, dim3(256), 0, st, a);
+  if (a.M > 128 && cdiv(a.N, 128) * cdiv(a.M, 128) >= 256) {
+    const dim3 grid(static_cast<unsigned>(cdiv(a.N, 128)), static_cast<unsigned>(cdiv(a.M, 128)));
+    hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 128, 128, 64>), grid, dim3(256), 0, st, a);
     return check_launch("dq_tile");
   }
-  if (a.M <= 64) return launch_split<BITS, BF16, 32, 64, 8>(st, a);
+  const int64_t t64 = cdiv(a.N, 64) * cdiv(a.M, 64);
+  if (t64 >= 192) {
+    const dim3 grid(static_cast<unsigned>(cdiv(a.N, 64)), static_cast<unsigned>(cdiv(a.M, 64)));
+    if (t64 <= 512) {
+      hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 64, 64, 128>), grid, dim3(256), 0, st, a);
+    } else if (a.M > 64) {
+      // beyond 512 tiles, 64 x 128 tiles (64-column steps) re-read each
+      // weight row half as often
+      const dim3 g2(static_cast<unsigned>(cdiv(a.N, 64)), static_cast<unsigned>(cdiv(a.M, 128)));
+      hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 64, 128, 64>), g2, dim3(256), 0, st, a);
+    } else {
+      hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 64, 64, 64>), grid, dim3(256), 0, st, a);
+    }
+    return check_launch("dq_tile");
+  }
+  if (a.M <= 32) return launch_split<BITS, BF16, 16, 32, 8>(st, a);
+  if (a.M <= 64) return launch_split<BITS, BF16, 16, 64, 8>(st, a);
   return launch_split<BITS, BF16, 16, 128, 8>(st, a);
 }
 

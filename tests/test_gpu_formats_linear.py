@@ -233,7 +233,10 @@ def test_triton_quantized_linear(hip):
                                       # tiled kernel: 64-row tiles with 128-column steps (odd step
                                       # count) and with 64-column steps, 128-row tiles
                                       (40, 8200, 512, 128), (128, 8256, 384, 128), (64, 16448, 384, 128),
-                                      (100, 16448, 640, 128), (130, 16448, 256, 128), (64, 32832, 256, 128)])
+                                      (100, 16448, 640, 128), (130, 16448, 256, 128), (64, 32832, 256, 128),
+                                      # split-K with 32-row M tiles; 64 x 64 tiles and split-K for M > 128
+                                      (24, 4100, 1024, 128), (32, 1000, 512, 64), (160, 4100, 512, 128),
+                                      (200, 2000, 512, 128)])
 def test_linear_dequant_gemm(hip, xdt, bits, M, N, K, gs):
     """M > 4: dequantise-then-MFMA kernels (split-K and tiled), ragged N and M,
     groups of 32-128 (one group per 32-code chunk), bias."""
