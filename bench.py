@@ -17,6 +17,8 @@ measured) and a CPU baseline: the CPU oracle timed on a bounded sample on
 this host's cores and extrapolated to one block.
 
     python bench.py [--steps 3] [--warmup 1] [--no-cpu] [--no-gemv]
+    python bench.py --workload opt125m     # config 2: whole OPT-125m-shaped model
+    python bench.py --workload llama13b    # config 5: whole 13B-shaped model, 2/4/8 bits
 """
 from __future__ import annotations
 
@@ -370,6 +372,98 @@ def cpu_baseline(seconds_hint=20.0):
                          "sweep_4096x1024": round(t_s, 3)}}
 
 
+# ------------------------------------------------ whole-model workloads --
+# Config 2 (OPT-125m shape) and config 5 (13B shape): random-init models built
+# from transformers' architectures, calibrated on uniform random token ids and
+# quantized layer by layer by DistributedGPTQuantizer.quantize_model (the
+# reference's core/quantizer.py:79-165 flow: calibration forward with hooks,
+# then every decoder Linear).  lm_head is not quantized (N > K: the
+# reference's quantize() cannot run it).
+MODELS = {
+    "opt125m": {"arch": "opt", "layers": 12, "hidden": 768, "heads": 12, "ffn": 3072, "vocab": 50272,
+                "nseq": 128, "seed": 1, "chunk": 16, "runs": [(4, 128, False)]},
+    "llama13b": {"arch": "llama", "layers": 40, "hidden": 5120, "heads": 40, "ffn": 13824, "vocab": 32000,
+                 "nseq": 256, "seed": 4, "chunk": 8, "runs": [(2, 64, True), (4, 128, True), (8, -1, True)]},
+}
+
+
+def build_model(spec, torch, dev):
+    """Random-init fp16 model of the named shape, weights ~N(0, 0.02^2)."""
+    from transformers import LlamaConfig, LlamaForCausalLM, OPTConfig, OPTForCausalLM
+    torch.manual_seed(spec["seed"])
+    if spec["arch"] == "opt":
+        cfg = OPTConfig(vocab_size=spec["vocab"], hidden_size=spec["hidden"], num_hidden_layers=spec["layers"],
+                        ffn_dim=spec["ffn"], num_attention_heads=spec["heads"], max_position_embeddings=2048,
+                        word_embed_proj_dim=spec["hidden"], init_std=0.02, use_cache=False)
+        cls = OPTForCausalLM
+    else:
+        cfg = LlamaConfig(vocab_size=spec["vocab"], hidden_size=spec["hidden"], intermediate_size=spec["ffn"],
+                          num_hidden_layers=spec["layers"], num_attention_heads=spec["heads"],
+                          num_key_value_heads=spec["heads"], max_position_embeddings=2048,
+                          initializer_range=0.02, use_cache=False)
+        cls = LlamaForCausalLM
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float16)
+    try:
+        with torch.device(dev):
+            model = cls(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    return model.eval()
+
+
+def decoder_linears(model, torch):
+    """Every nn.Linear inside the decoder layers (lm_head excluded)."""
+    return [n for n, m in model.named_modules() if isinstance(m, torch.nn.Linear) and ".layers." in n]
+
+
+def run_model(args, torch, dev):
+    import copy
+
+    from distributed_gptq_amd import DistributedGPTQuantizer, QuantizationConfig
+    spec = MODELS[args.workload]
+    nseq = args.model_nseq or spec["nseq"]
+    log(f"[bench] {args.workload}: building the random-init model")
+    base = build_model(spec, torch, dev)
+    names = decoder_linears(base, torch)
+    g = torch.Generator(device=dev).manual_seed(spec["seed"])
+    ids = torch.randint(0, spec["vocab"], (nseq, args.seqlen), device=dev, generator=g)
+    chunk = spec["chunk"]
+    data = [ids[i:i + chunk] for i in range(0, nseq, chunk)]
+    runs = []
+    # untimed warm-up runs of the first setting (library initialisation, GEMM heuristics)
+    settings = [spec["runs"][0]] * args.warmup + list(spec["runs"])
+    for idx, (bits, gs, actorder) in enumerate(settings):
+        timed = idx >= args.warmup
+        model = copy.deepcopy(base)
+        cfg = QuantizationConfig(bits=bits, group_size=gs, actorder=actorder, calibration_samples=nseq)
+        dq = DistributedGPTQuantizer(cfg)
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        free0, total = torch.cuda.mem_get_info()
+        t0 = time.perf_counter()
+        def progress(done, total, name, stats):
+            if done % 28 == 0 or done == total:
+                log(f"[bench]   {done}/{total} layers quantized ({time.perf_counter() - t0:.1f} s)")
+
+        dq.quantize_model(model, data, layers_to_quantize=names, progress_callback=progress)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        free1, _ = torch.cuda.mem_get_info()
+        errs = dq.quantization_errors
+        r = {"bits": bits, "group_size": gs, "actorder": actorder, "wall_s": round(wall, 3),
+             "layers": len(errs), "peak_allocated_GiB": round(torch.cuda.max_memory_allocated() / 2**30, 2),
+             "device_used_GiB_after": round((total - free1) / 2**30, 2),
+             "total_error": float(sum(errs.values()))}
+        log(f"[bench] {args.workload} w{bits} g{gs}{'' if timed else ' (warm-up)'}: {r}")
+        if timed:
+            runs.append(r)
+        del model, dq
+        torch.cuda.empty_cache()
+    return {"runs": runs, "nseq": nseq, "layers": len(names), "chunk": chunk,
+            "params_GiB": round(sum(p.numel() for p in base.parameters()) * 2 / 2**30, 2)}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -385,6 +479,9 @@ def main():
     ap.add_argument("--no-gemv", action="store_true")
     ap.add_argument("--no-block", action="store_true")
     ap.add_argument("--no-3bit", action="store_true", help="skip the 3-bit block run")
+    ap.add_argument("--workload", choices=["block", *MODELS], default="block",
+                    help="block: config 3 (default); opt125m: config 2; llama13b: config 5")
+    ap.add_argument("--model-nseq", type=int, default=0, help="calibration sequences for a model workload")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -397,6 +494,23 @@ def main():
     import distributed_gptq_amd  # noqa: F401
     from distributed_gptq_amd import _lib
     _lib.load()
+    if args.workload != "block":
+        m = run_model(args, torch, dev)
+        spec = MODELS[args.workload]
+        first = m["runs"][0]
+        print(json.dumps({
+            "metric": f"s per {args.workload}-shaped model quantized (calibration forward + Hessians + every decoder Linear)",
+            "value": first["wall_s"], "unit": "s/model", "n_gpus": 1, "steps": 1, "warmup": args.warmup,
+            "ms_per_step": round(first["wall_s"] * 1e3, 1), "higher_is_better": False, "scaling": "weak",
+            "vs_baseline": None, "dtype": "fp16",
+            "data": "synthetic (random-init weights N(0,0.02^2), uniform random token ids)",
+            "config": {"workload": args.workload, "layers": spec["layers"], "hidden": spec["hidden"],
+                       "heads": spec["heads"], "ffn": spec["ffn"], "vocab": spec["vocab"], "nseq": m["nseq"],
+                       "seq_len": args.seqlen, "sequences_per_forward": m["chunk"],
+                       "quantized_linears": m["layers"], "params_GiB": m["params_GiB"],
+                       "parallelism": "single-gpu"},
+            "runs": m["runs"]}), flush=True)
+        return
     result = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
               "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
               "data": "synthetic (random-init weights, N(0,1) calibration with RMSNorm outlier channels)",

@@ -307,3 +307,49 @@ def test_shared_and_separate_hessians_bit_identical(hip):
         if isinstance(ma, nn.Linear):
             assert torch.equal(ma.weight, mb.weight), n
             assert not torch.equal(ma.weight, dict(base.named_modules())[n].weight), n
+
+
+@pytest.mark.gpu
+def test_transformers_opt_model_end_to_end(hip):
+    """Config 2's flow at a small size: a random-init transformers OPT model
+    (the architecture of the reference's examples/single_gpu_example.py:53-59,
+    built locally) calibrated on token ids, every decoder Linear quantized by
+    quantize_model.  Each layer is bit-identical to a per-layer GPTQ fed the
+    inputs the hooks saw; lm_head stays unquantized; the quantized model's
+    logits stay near the fp16 model's."""
+    import copy
+
+    transformers = pytest.importorskip("transformers")
+    from distributed_gptq_amd import GPTQ, DistributedGPTQuantizer, QuantizationConfig
+    from distributed_gptq_amd.models.layers import QuantizedLinear
+    torch.manual_seed(3)
+    cfg = transformers.OPTConfig(vocab_size=512, hidden_size=128, num_hidden_layers=2, ffn_dim=256,
+                                 num_attention_heads=4, max_position_embeddings=128, word_embed_proj_dim=128,
+                                 init_std=0.02, use_cache=False)
+    base = transformers.OPTForCausalLM(cfg).cuda().half().eval()
+    g = torch.Generator(device="cuda").manual_seed(1)
+    data = [torch.randint(0, 512, (2, 64), device="cuda", generator=g) for _ in range(4)]
+    names = [n for n, m in base.named_modules() if isinstance(m, nn.Linear) and ".layers." in n]
+    assert len(names) == 12
+    xs, _, ns = _capture(base, data)
+    model = copy.deepcopy(base)
+    dq = DistributedGPTQuantizer(QuantizationConfig(bits=4, group_size=64, actorder=False))
+    dq.quantize_model(model, data, layers_to_quantize=names)
+    mods, ref_mods = dict(model.named_modules()), dict(copy.deepcopy(base).named_modules())
+    assert isinstance(mods["lm_head"], nn.Linear)
+    for n in names:
+        q = mods[n]
+        assert isinstance(q, QuantizedLinear), n
+        gq = GPTQ(ref_mods[n], bits=4, group_size=64, device="cuda", token_buffer=0)
+        for x in xs[n]:
+            gq.add_batch(x)
+        gq.fasterquant()
+        r = QuantizedLinear.from_gptq(gq)
+        for f in ("qweight", "scales", "zeros", "g_idx"):
+            assert torch.equal(getattr(q, f), getattr(r, f)), (n, f)
+        assert dq.quantized_layers[n]["nsamples"] == ns[n] == 8
+    ids = torch.randint(0, 512, (1, 64), device="cuda", generator=g)
+    with torch.no_grad():
+        a, b = base(ids).logits.float(), model(ids).logits.float()
+    assert torch.isfinite(b).all()
+    assert ((a - b).norm() / a.norm()).item() < 0.2
