@@ -259,13 +259,38 @@ __host__ __device__ constexpr int pair_b(int p) {
   return pair_a<BITS>(p) + (BITS == 4 ? 4 : BITS == 2 ? 8 : BITS == 8 ? 2 : 16);
 }
 
+// 3-bit codes with fp16 activations pair code k with code k + 8 (k in 0..7,
+// 16..23): 24 bits apart, so both sit at the same offset (3k mod 8) inside
+// their bytes.  One byte permute gathers the two 16-bit windows that hold
+// them, one and-or masks them under the magic exponent (1024 + 2^s * code,
+// exact for s <= 7), and the pair's class is its bit offset s.
+__host__ __device__ constexpr int p3_lo(int p) { return p < 8 ? p : p + 8; }
+
 template <int BITS, bool BF16>
 struct M1Fmt {
-  // scale classes: fp16 4-bit pairs alternate x1 / x16; fp16 2-bit cycle x1 x4 x16 x64
-  static constexpr int NCLS = BF16 ? 1 : BITS == 4 ? 2 : BITS == 2 ? 4 : 1;
+  static constexpr bool kPerm3 = BITS == 3 && !BF16;
+  // scale classes: fp16 4-bit pairs alternate x1 / x16; fp16 2-bit cycle x1 x4 x16 x64;
+  // fp16 3-bit pairs carry 2^s for their bit offset s in 0..7
+  static constexpr int NCLS = BF16 ? 1 : BITS == 4 ? 2 : BITS == 2 ? 4 : BITS == 3 ? 8 : 1;
   static constexpr float kOff = BF16 ? (BITS == 8 ? 0.0f : 128.0f) : 1024.0f;
-  static constexpr int cls(int p) { return p % NCLS; }
-  static constexpr float mult(int c) { return static_cast<float>(1 << (BITS * c)); }
+  static constexpr int cls(int p) { return kPerm3 ? (3 * p3_lo(p)) % 8 : p % NCLS; }
+  static constexpr float mult(int c) { return static_cast<float>(1 << (kPerm3 ? c : BITS * c)); }
+  static constexpr int pa(int p) { return kPerm3 ? p3_lo(p) : pair_a<BITS>(p); }
+  static constexpr int pb(int p) { return kPerm3 ? p3_lo(p) + 8 : pair_b<BITS>(p); }
+};
+
+// byte-permute selector and source dword of fp16 3-bit pair P: output bytes
+// (j, j + 1, j + 3, j + 4) of the 12-byte chunk, j = 3k / 8, read from the
+// dword pair (d, d + 1); a byte the code does not reach selects zero (0x0c)
+template <int P>
+struct Perm3 {
+  static constexpr int k = p3_lo(P), j = 3 * k / 8, s = 3 * k % 8;
+  static constexpr int d = j / 4 < 1 ? 0 : 1;
+  static constexpr uint32_t byte(int b, bool need) { return need ? static_cast<uint32_t>(b - 4 * d) : 0x0cu; }
+  static constexpr uint32_t sel = byte(j, true) | (byte(j + 1, s + 3 > 8) << 8) | (byte(j + 3, true) << 16) |
+                                  (byte(j + 4, s + 3 > 8) << 24);
+  static constexpr uint32_t mask = (7u << s) | (7u << (s + 16));
+  static_assert(j + 3 - 4 * d <= 7 && (s + 3 <= 8 || j + 4 - 4 * d <= 7), "3-bit pair outside its dword pair");
 };
 
 // pair P of the chunk with the magic exponent already or-ed in
@@ -292,6 +317,10 @@ __device__ __forceinline__ uint32_t m1_pair(const uint32_t* dw, uint32_t magic) 
     const uint32_t w = dw[d] >> (8 * i);
     if constexpr (!BF16) return (w & 0x00FF00FFu) | magic;
     else return bf16_pair_exact(w & 0x00FF00FFu);
+  } else if constexpr (!BF16) {
+    using Q = Perm3<P>;
+    const uint32_t t = __builtin_amdgcn_perm(dw[Q::d + 1], dw[Q::d], Q::sel);
+    return (t & Q::mask) | magic;
   } else {
     // 3-bit: code P at bit 3P, code P + 16 at bit 3P + 48 (funnel shifts)
     constexpr int b0 = 3 * P, b1 = 3 * P + 32;
@@ -338,7 +367,7 @@ __device__ __forceinline__ void prep_x_chunk(const u32x4 (&raw)[4], uint32_t (&x
   }
 #pragma unroll
   for (int p = 0; p < 16; ++p) {
-    const int ia = pair_a<BITS>(p), ib = pair_b<BITS>(p);
+    const int ia = F::pa(p), ib = F::pb(p);
     const uint32_t lo = (d[ia >> 1] >> (16 * (ia & 1))) & 0xffffu;
     const uint32_t hi = (d[ib >> 1] >> (16 * (ib & 1))) & 0xffffu;
     xr[p] = lo | (hi << 16);
@@ -1471,7 +1500,8 @@ __global__ __launch_bounds__(256) void linear_generic(const void* __restrict__ x
 
 template <int BITS, bool BF16, bool SZBF, int MAXC, int WS>
 int launch_m1(hipStream_t st, const LinArgs& a) {
-  // rows per batch: at most 16 code dwords per lane and buffer (measured best on MI355X)
+  // rows per batch: at most 16 code dwords per lane and buffer (measured best on MI355X;
+  // 24 for 3-bit codes measured 11-28% slower: uneven batches per wave)
   constexpr int kBudget = 16;
   constexpr int kFit = kBudget / (MAXC * BITS) > 0 ? kBudget / (MAXC * BITS) : 1;
   constexpr int RB = kFit >= 8 ? 8 : kFit >= 4 ? 4 : kFit >= 2 ? 2 : 1;
