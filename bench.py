@@ -428,7 +428,7 @@ def run_model(args, torch, dev):
     names = decoder_linears(base, torch)
     g = torch.Generator(device=dev).manual_seed(spec["seed"])
     ids = torch.randint(0, spec["vocab"], (nseq, args.seqlen), device=dev, generator=g)
-    chunk = spec["chunk"]
+    chunk = args.model_chunk or spec["chunk"]
     data = [ids[i:i + chunk] for i in range(0, nseq, chunk)]
     runs = []
     # untimed warm-up runs of the first setting (library initialisation, GEMM heuristics)
@@ -482,6 +482,7 @@ def main():
     ap.add_argument("--workload", choices=["block", *MODELS], default="block",
                     help="block: config 3 (default); opt125m: config 2; llama13b: config 5")
     ap.add_argument("--model-nseq", type=int, default=0, help="calibration sequences for a model workload")
+    ap.add_argument("--model-chunk", type=int, default=0, help="sequences per calibration forward (model workloads)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
