@@ -283,12 +283,15 @@ def gemv_bytes(N, K, bits, M=1):
     return N * K * bits // 8 + N * (K // 128) * 4 + M * K * 2 + M * N * 2
 
 
-def run_gemv(args, torch, dev, bits, M=1, min_bytes=1 << 30, reps=3):
+def run_gemv(args, torch, dev, bits, M=1, min_bytes=1 << 30, reps=3, actorder=False):
+    """Per-launch time of gptq_linear (act-order: gptq_linear_perm, weights
+    stored in sweep order and x gathered through a random permutation) at
+    the config-4 shapes, inside a HIP graph, rotating >= 1 GiB of weights."""
     from distributed_gptq_amd import _ops
     out = {}
     g = torch.Generator(device=dev).manual_seed(3)
     for (N, K) in GEMV_SHAPES:
-        nbytes = gemv_bytes(N, K, bits, M)
+        nbytes = gemv_bytes(N, K, bits, M) + (K * 4 if actorder else 0)
         R = max(2, math.ceil(min_bytes / (N * K * bits // 8)))
         codes = torch.randint(0, 2 ** bits, (N, K), generator=g, device=dev, dtype=torch.uint8)
         q0 = _ops.pack(codes, bits)
@@ -297,16 +300,17 @@ def run_gemv(args, torch, dev, bits, M=1, min_bytes=1 << 30, reps=3):
         zr = torch.full((N, K // 128), float(2 ** (bits - 1)), device=dev, dtype=torch.float16)
         x = torch.randn(M, K, generator=g, device=dev, dtype=torch.float32).half()
         y = torch.empty(M, N, device=dev, dtype=torch.float16)
-        for r in range(R):
-            _ops.linear(x, qs[r], bits, sc[r], zr, K, group_size=128, out=y)
-        torch.cuda.synchronize()
+        perm = torch.randperm(K, generator=g, device=dev).to(torch.int32) if actorder else None
         graph = torch.cuda.CUDAGraph()
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
+            for r in range(R):  # warm-up (and the workspace of this stream) outside the capture
+                _ops.linear(x, qs[r], bits, sc[r], zr, K, group_size=128, out=y, perm=perm)
+            s.synchronize()
             with torch.cuda.graph(graph, stream=s):
                 for r in range(R):
-                    _ops.linear(x, qs[r], bits, sc[r], zr, K, group_size=128, out=y)
+                    _ops.linear(x, qs[r], bits, sc[r], zr, K, group_size=128, out=y, perm=perm)
         torch.cuda.current_stream().wait_stream(s)
         graph.replay()
         torch.cuda.synchronize()
@@ -328,6 +332,26 @@ def run_gemv(args, torch, dev, bits, M=1, min_bytes=1 << 30, reps=3):
 
 
 # ------------------------------------------------------------ CPU baseline --
+
+def _host_cpu():
+    """CPU model, physical / logical cores and the cores this process may use."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        import psutil
+        physical = psutil.cpu_count(logical=False)
+    except Exception:  # noqa: BLE001 -- psutil missing or restricted
+        physical = None
+    return {"cpu_model": model, "physical_cores": physical, "logical_cores": os.cpu_count(),
+            "affinity_cores": len(os.sched_getaffinity(0))}
+
 
 def cpu_baseline(seconds_hint=20.0):
     """The CPU oracle (numpy, this host's BLAS threads) on a bounded sample of
@@ -363,6 +387,8 @@ def cpu_baseline(seconds_hint=20.0):
     swp = sum(t_s * (n / 4096) * (k / 1024) ** 2 for n, k in layers)
     total = hess + fac + swp
     return {"value": round(total, 2), "unit": "s/block", "cores": threads, "kind": "port",
+            "host": _host_cpu(),
+            "mode": "canonical GPTQ with act-order (the block's setting), oracle in fp32",
             "sample": ("oracle/gptq_oracle.py in numpy fp32 on 2 x 2048 tokens (Hessian, K=4096), one damped "
                        "Cholesky inverse at K=4096, one act-order sweep of 4096 x 1024; extrapolated per Linear "
                        "of the block (Hessian x 128 sequences x (K/4096)^2, inverse x (K/4096)^3, sweep x "
@@ -567,6 +593,12 @@ def main():
                 gm, _ = run_gemv(args, torch, dev, bits, M=M)
                 result["gemv"][f"w{bits}a16_m{M}"] = gm
                 log(f"[bench] W{bits}A16 M={M}: {gm}")
+        # act-order layers (GPTQ output with act-order, the block's own
+        # setting): sweep-order storage, x gathered through the permutation
+        for M in (1, 16, 128):
+            gm, _ = run_gemv(args, torch, dev, 4, M=M, actorder=True)
+            result["gemv"][f"w4a16_actorder_m{M}"] = gm
+            log(f"[bench] W4A16 act-order M={M}: {gm}")
     if args.no_block:
         result.setdefault("value", None)
     if not args.no_cpu:

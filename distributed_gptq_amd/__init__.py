@@ -9,13 +9,15 @@ gptq::linear operator) and ``kernels``; ``core.checkpoint`` holds the
 reference quantizer's save/load (safetensors + JSON sidecar).
 """
 from .core.gptq import GPTQ, GPTQMultiGPU, quantize_layer_gptq
-from .core.quantizer import DistributedGPTQuantizer, QuantizationConfig, Quantizer, quantize_model_simple
-from .core.dequantizer import GPTQDequantizer
+from .core.quantizer import (DistributedConfig, DistributedGPTQuantizer, QuantizationConfig, QuantizationMode,
+                             Quantizer, create_distributed_config, quantize_model_simple)
+from .core.dequantizer import GPTQDequantizer, dequantize_model
 
 __version__ = "0.1.0"
 
-__all__ = ["GPTQ", "GPTQMultiGPU", "quantize_layer_gptq", "DistributedGPTQuantizer", "QuantizationConfig", "Quantizer",
-           "quantize_model_simple", "GPTQDequantizer",
+__all__ = ["__version__", "GPTQ", "GPTQMultiGPU", "quantize_layer_gptq", "DistributedGPTQuantizer",
+           "QuantizationConfig", "Quantizer", "quantize_model_simple", "GPTQDequantizer", "dequantize_model",
+           "DistributedConfig", "QuantizationMode", "create_distributed_config",
            "QuantizedLinear", "replace_with_quantized_layers", "save_quantized_model", "load_quantized_model"]
 
 

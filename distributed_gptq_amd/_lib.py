@@ -52,6 +52,9 @@ SIGNATURES = {
     "gptq_pack_reference_layout": (_i, [_p, _i64, _i64, _i, _p, _p]),
     "gptq_dequant": (_i, [_p, _i, _p, _p, _i, _p, _i, _i64, _i64, _i64, _p, _p]),
     "gptq_linear": (_i, [_p, _i, _i64, _p, _i, _p, _p, _i, _p, _i, _i64, _p, _i, _i64, _i64, _p, _p]),
+    "gptq_linear_perm_workspace_size": (_sz, [_i64, _i64, _i]),
+    "gptq_linear_perm": (_i, [_p, _i, _i64, _p, _p, _i, _p, _p, _i, _p, _i, _i64, _p, _i, _i64, _i64, _p, _p, _sz,
+                              _p]),
     "gptq_quantize_tensor": (_i, [_p, _i, _i64, _i, _i, _i, _p, _p, _p, _p]),
     "gptq_dequantize_tensor": (_i, [_p, _i64, _i, _p, _p, _p, _p]),
 }

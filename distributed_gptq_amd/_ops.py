@@ -244,8 +244,10 @@ def dequant(packed: torch.Tensor, bits: int, scales: torch.Tensor, zeros: torch.
 
 def linear(x: torch.Tensor, packed: torch.Tensor, bits: int, scales: torch.Tensor, zeros: torch.Tensor, K: int,
            g_idx: torch.Tensor | None = None, group_size: int = 0, bias: torch.Tensor | None = None,
-           out: torch.Tensor | None = None) -> torch.Tensor:
-    """y = x @ dequant(W)^T (+ bias), x (..., K) -> (..., N) in x.dtype."""
+           out: torch.Tensor | None = None, perm: torch.Tensor | None = None) -> torch.Tensor:
+    """y = x @ dequant(W)^T (+ bias), x (..., K) -> (..., N) in x.dtype.
+    With ``perm`` (act-order storage: weight column j holds input column
+    perm[j]) y = x[..., perm] @ dequant(W)^T (+ bias)."""
     _gpu(x, packed, scales, zeros)
     lead = x.shape[:-1]
     x2 = x.reshape(-1, K)
@@ -260,9 +262,19 @@ def linear(x: torch.Tensor, packed: torch.Tensor, bits: int, scales: torch.Tenso
     if bias is not None:
         bias = bias.contiguous()
     y = out if out is not None else torch.empty((M, N), dtype=x.dtype, device=x.device)
-    L.call("gptq_linear", _p(x2), dtype_code(x2.dtype), M, _p(packed), bits, _p(scales), _p(zeros),
+    if perm is None:
+        L.call("gptq_linear", _p(x2), dtype_code(x2.dtype), M, _p(packed), bits, _p(scales), _p(zeros),
+               dtype_code(scales.dtype), _p(g_idx), group_size, scales.shape[1], _p(bias),
+               dtype_code(bias.dtype) if bias is not None else 0, N, K, _p(y), _stream(x.device))
+        return y.reshape(*lead, N)
+    perm = perm.to(device=x.device, dtype=torch.int32).contiguous()
+    if perm.numel() != K:
+        raise ValueError(f"perm has {perm.numel()} entries, in_features is {K}")
+    nb = L.lib().gptq_linear_perm_workspace_size(M, K, dtype_code(x2.dtype))
+    ws = workspace(nb, x.device)
+    L.call("gptq_linear_perm", _p(x2), dtype_code(x2.dtype), M, _p(perm), _p(packed), bits, _p(scales), _p(zeros),
            dtype_code(scales.dtype), _p(g_idx), group_size, scales.shape[1], _p(bias),
-           dtype_code(bias.dtype) if bias is not None else 0, N, K, _p(y), _stream(x.device))
+           dtype_code(bias.dtype) if bias is not None else 0, N, K, _p(y), _p(ws), ws.numel(), _stream(x.device))
     return y.reshape(*lead, N)
 
 

@@ -55,15 +55,22 @@ def _layer_info(m: QuantizedLinear) -> dict:
             "in_features": int(m.in_features), "out_features": int(m.out_features), "bias": m.bias is not None}
 
 
+# the reference's QuantizationConfig fields (core/quantizer.py:27-34): the
+# sidecar holds exactly these, so the reference's loader can read it
+_REF_CONFIG_KEYS = ("bits", "group_size", "actorder", "percdamp", "blocksize", "calibration_samples", "use_triton",
+                    "save_packed")
+
+
 def _config_dict(config: Union[QuantizationConfig, dict, None], qmods: Dict[str, QuantizedLinear]) -> dict:
     if isinstance(config, QuantizationConfig):
-        return asdict(config)
-    if isinstance(config, dict):
-        return asdict(QuantizationConfig(**config))
-    first = next(iter(qmods.values()), None)
-    if first is None:
-        return asdict(QuantizationConfig())
-    return asdict(QuantizationConfig(bits=first.bits, group_size=first.group_size))
+        d = asdict(config)
+    elif isinstance(config, dict):
+        d = asdict(QuantizationConfig(**config))
+    else:
+        first = next(iter(qmods.values()), None)
+        d = asdict(QuantizationConfig() if first is None else
+                   QuantizationConfig(bits=first.bits, group_size=first.group_size))
+    return {k: d[k] for k in _REF_CONFIG_KEYS}
 
 
 def _cpu_state(model: nn.Module) -> Dict[str, torch.Tensor]:
@@ -147,6 +154,9 @@ def _check_buffers(name: str, info: dict, state: Dict[str, torch.Tensor]) -> Non
             raise ValueError(f"{name}.{key}: saved shape {tuple(t.shape)}, layout wants {shape}")
     if info["bias"] != (f"{name}.bias" in state):
         raise ValueError(f"{name}: bias presence differs between the sidecar and the state dict")
+    perm = state.get(f"{name}.perm")
+    if perm is not None and tuple(perm.shape) not in ((0,), (K,)):
+        raise ValueError(f"{name}.perm: saved shape {tuple(perm.shape)}, expected (0,) or ({K},)")
 
 
 def _install(model: nn.Module, name: str, info: dict, state: Dict[str, torch.Tensor]) -> None:
@@ -172,7 +182,8 @@ def _install(model: nn.Module, name: str, info: dict, state: Dict[str, torch.Ten
         setattr(parent, parts[-1], q)
     else:
         raise TypeError(f"{name}: expected nn.Linear or QuantizedLinear, found {type(old).__name__}")
-    for key in _BUFFERS + (("bias",) if info["bias"] else ()):
+    extra = (("bias",) if info["bias"] else ()) + (("perm",) if f"{name}.perm" in state else ())
+    for key in _BUFFERS + extra:
         t = state[f"{name}.{key}"]
         getattr(q, key).data = torch.empty(t.shape, dtype=t.dtype, device=device)
 

@@ -1,4 +1,4 @@
-"""GPTQDequantizer (src/distributed_gptq/core/dequantizer.py:14-89).
+"""GPTQDequantizer and dequantize_model (src/distributed_gptq/core/dequantizer.py:14-163).
 
 ``dequantize_weight`` computes (q - zeros) * scales in fp32 with the 4-bit
 low-nibble-first unpack of ``_unpack_4bit`` (:68-89); both run in the HIP
@@ -52,3 +52,18 @@ class GPTQDequantizer:
         if layer.bias is not None:
             out.bias.data = layer.bias.data.float()
         return out
+
+    def dequantize_model(self, model: nn.Module) -> nn.Module:
+        """Every QuantizedLinear of ``model`` replaced by an nn.Linear holding
+        its fp32 dequantised weights (:123-142); returns ``model``."""
+        for name, child in model.named_children():
+            if len(list(child.children())) > 0:
+                setattr(model, name, self.dequantize_model(child))
+            else:
+                setattr(model, name, self.dequantize_layer(child))
+        return model
+
+
+def dequantize_model(model: nn.Module, bits: int = 4, group_size: int = 128) -> nn.Module:
+    """:145-163."""
+    return GPTQDequantizer(bits=bits, group_size=group_size).dequantize_model(model)

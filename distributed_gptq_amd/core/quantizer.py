@@ -15,6 +15,7 @@ from __future__ import annotations
 import logging
 import time
 from dataclasses import asdict, dataclass
+from enum import Enum
 from typing import Any, Callable, Dict, List, Optional, Tuple, Union
 
 import torch
@@ -37,6 +38,11 @@ class QuantizationConfig:
     calibration_samples: int = 128
     use_triton: bool = False
     save_packed: bool = True
+    # quantize block by block, and the layer groups of a block one after
+    # another, each calibrated on the quantized predecessors' outputs (the
+    # reference CLI's --true-sequential, cli.py:207-211, which its config
+    # lacks)
+    true_sequential: bool = False
 
     def __post_init__(self):
         self.validate()
@@ -142,6 +148,54 @@ class Quantizer(nn.Module):
         return bool(torch.all(self.scale != 0))
 
 
+# ------------------------------------------------- process configuration --
+
+class QuantizationMode(Enum):
+    """Processing modes (distributed/coordinator.py:21-26).  This build runs
+    one process on one GPU: only SINGLE_GPU is accepted by the driver."""
+    SINGLE_GPU = "single_gpu"
+    DATA_PARALLEL = "data_parallel"
+    MODEL_PARALLEL = "model_parallel"
+    PIPELINE_PARALLEL = "pipeline_parallel"
+
+
+@dataclass
+class DistributedConfig:
+    """Process configuration (distributed/coordinator.py:29-47), accepted by
+    DistributedGPTQuantizer; world_size must be 1 here."""
+    mode: QuantizationMode = QuantizationMode.SINGLE_GPU
+    world_size: int = 1
+    rank: int = 0
+    local_rank: int = 0
+    master_addr: str = "localhost"
+    master_port: str = "12355"
+    backend: str = "nccl"
+    init_timeout: int = 1800
+
+    @property
+    def is_distributed(self) -> bool:
+        return self.world_size > 1
+
+    @property
+    def is_main_process(self) -> bool:
+        return self.rank == 0
+
+
+def create_distributed_config(mode: Union[str, QuantizationMode] = "auto") -> DistributedConfig:
+    """From the launcher's environment (WORLD_SIZE, RANK, LOCAL_RANK,
+    MASTER_ADDR, MASTER_PORT), as distributed/coordinator.py:264-301."""
+    import os
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if mode == "auto":
+        mode = QuantizationMode.SINGLE_GPU if world == 1 else QuantizationMode.DATA_PARALLEL
+    elif isinstance(mode, str):
+        mode = QuantizationMode(mode)
+    return DistributedConfig(mode=mode, world_size=world, rank=int(os.environ.get("RANK", "0")),
+                             local_rank=int(os.environ.get("LOCAL_RANK", "0")),
+                             master_addr=os.environ.get("MASTER_ADDR", "localhost"),
+                             master_port=os.environ.get("MASTER_PORT", "12355"))
+
+
 # ------------------------------------------------------------- driver --
 
 class _HookError(RuntimeError):
@@ -149,18 +203,36 @@ class _HookError(RuntimeError):
     calibration batch)."""
 
 
+class _StopForward(Exception):
+    """Ends a calibration forward once the first block's inputs are taken."""
+
+
+def _find_blocks(model: nn.Module, layers: Dict[str, nn.Linear]):
+    """(name, ModuleList) of the module list whose entries hold the most of
+    ``layers`` (a transformer's decoder blocks), or None."""
+    best, best_n = None, 0
+    for name, mod in model.named_modules():
+        if isinstance(mod, nn.ModuleList) and len(mod) > 0 and name:
+            n = sum(1 for k in layers if k.startswith(name + "."))
+            if n > best_n:
+                best, best_n = (name, mod), n
+    return best
+
+
 class _SharedHessians:
     """Hessians of a calibration pass, one per group of layers that received
     the same input tensor in every batch so far (q/k/v, gate/up).
 
     Every layer starts alone.  A layer with no samples yet joins a group
-    that also had none before this batch and was just given the same tensor
-    (both Hessians are then that tensor's X^T X).  A group of several layers
+    that also had none before this batch and has been given the same tensor,
+    and nothing else, in it (both Hessians are then that tensor's X^T X).
+    A group of several layers
     adds its input once every member has seen the batch: members whose input
     differs from the first member's leave the group with a copy of the
     group's Hessian as it was before this batch (exact: nothing of this batch
     has been added yet), and each distinct input is added once.  Inputs are
-    compared by storage, offset, shape, stride, dtype and version counter;
+    compared by storage, offset, shape, stride, dtype and version counter
+    (inference tensors, which have none: and by value against a clone);
     a group's pending inputs are kept referenced (so a reused allocation
     cannot pass for the same input) and cloned (so an in-place change after
     the first member's call is seen as a different input, not lost).  With
@@ -185,6 +257,7 @@ class _SharedHessians:
         # and key -> (group, input) for groups that had no samples before it
         self.pending: Dict[int, Dict[tuple, Tuple[torch.Tensor, torch.Tensor, List[str]]]] = {}
         self.fresh: Dict[tuple, Tuple[int, torch.Tensor]] = {}
+        self.fresh_key: Dict[int, tuple] = {}
 
     def _new_group(self, names: List[str], copy_from) -> int:
         gid = len(self.acc)
@@ -199,23 +272,44 @@ class _SharedHessians:
 
     @staticmethod
     def _key(x: torch.Tensor) -> tuple:
+        # inference tensors (torch.inference_mode) have no version counter:
+        # an in-place change between two layers is then found by comparing
+        # values with a clone (_same)
         return (x.untyped_storage().data_ptr(), x.storage_offset(), tuple(x.shape), tuple(x.stride()), x.dtype,
-                x._version)
+                None if x.is_inference() else x._version)
+
+    @staticmethod
+    def _same(x: torch.Tensor, seen: torch.Tensor) -> bool:
+        """x has the key of ``seen`` (a clone taken at the earlier call):
+        the same tensor, unchanged, unless an inference tensor changed in
+        place (one comparison on the device)."""
+        return not x.is_inference() or bool(torch.equal(x, seen))
 
     def add(self, name: str, x: torch.Tensor) -> None:
         gid = self.group_of[name]
+        if not self.share:
+            self.acc[gid].add_batch(x)
+            return
         key = self._key(x)
         if len(self.members[gid]) == 1:
             acc = self.acc[gid]
-            if self.share and acc.nsamples == 0:
+            if acc.nsamples == 0:
                 hit = self.fresh.get(key)
-                if hit is not None and hit[0] != gid:
+                if hit is not None and hit[0] != gid and self._same(x, hit[1]):
                     g = hit[0]
                     self.members[g].append(name)
                     self.group_of[name] = g
                     self.members[gid] = []
                     return
-                self.fresh[key] = (gid, x)
+                self.fresh[key] = (gid, x.clone() if x.is_inference() else x)
+                self.fresh_key[gid] = key
+            else:
+                # a second tensor for this group in this batch: its Hessian is
+                # no longer that of the tensor it was registered under, so no
+                # later layer may join it
+                k0 = self.fresh_key.pop(gid, None)
+                if k0 is not None:
+                    self.fresh.pop(k0, None)
             acc.add_batch(x)
             return
         if any(name in names for _, _, names in self.pending.get(gid, {}).values()):
@@ -225,6 +319,8 @@ class _SharedHessians:
             self.add(name, x)
             return
         part = self.pending.setdefault(gid, {})
+        while key in part and not self._same(x, part[key][1]):
+            key = key + ("changed",)  # an inference tensor changed in place since
         if key not in part:
             part[key] = (x, x.clone(), [])
         part[key][2].append(name)
@@ -248,6 +344,7 @@ class _SharedHessians:
         for gid in list(self.pending):
             self._settle(gid)
         self.fresh.clear()
+        self.fresh_key.clear()
 
     def groups(self) -> Dict[int, List[str]]:
         return {g: list(m) for g, m in self.members.items() if m}
@@ -327,15 +424,51 @@ class DistributedGPTQuantizer:
             batch = batch[0]
         return batch
 
+    def _model_batches(self, model: nn.Module, calibration_data):
+        """Runs the calibration forwards of the whole model, at most
+        ``calibration_samples`` rows; yields once per batch (True if it ran,
+        False if it failed and was skipped, as the reference does, :232-236)."""
+        seen = 0
+        for batch in calibration_data:
+            if seen >= self.quant_config.calibration_samples:
+                break
+            b = self._inputs(batch)
+            try:
+                if isinstance(b, dict):
+                    b = {k: v.to(self.device) if torch.is_tensor(v) else v for k, v in b.items()}
+                    rows = next(v for v in b.values() if torch.is_tensor(v)).shape[0]
+                    model(**b)
+                else:
+                    b = b.to(self.device)
+                    rows = b.shape[0]
+                    model(b)
+                ok = True
+            except _HookError:
+                raise
+            except _StopForward:  # the first block's inputs are taken
+                rows = (b if torch.is_tensor(b) else next(v for v in b.values() if torch.is_tensor(v))).shape[0]
+                ok = True
+            except Exception as e:  # noqa: BLE001
+                logger.warning("error during calibration forward, batch skipped: %s", e)
+                rows, ok = 0, False
+            seen += rows
+            yield ok
+
     @torch.no_grad()
-    def _collect_hessians(self, model: nn.Module, calibration_data, layers: Dict[str, nn.Linear]) -> _SharedHessians:
+    def _collect_hessians(self, model: nn.Module, calibration_data, layers: Dict[str, nn.Linear],
+                          batches=None) -> _SharedHessians:
         """Calibration forward (:194-246) with the Hessians accumulated in the
-        hooks; stops once ``calibration_samples`` rows have been seen."""
+        hooks.  ``batches`` (an iterator that runs one forward per step and
+        yields whether it ran) defaults to the whole model over
+        ``calibration_data``."""
         hs = _SharedHessians(layers, self.device, self.share_hessians)
+        self._call_order: List[str] = []
 
         def hook_for(name):
             def hook(module, inp, out):
                 x = inp[0] if isinstance(inp, tuple) else inp
+                if name not in self._call_order:
+                    self._call_order.append(name)
                 try:
                     hs.add(name, x.detach())
                 except Exception as e:
@@ -343,30 +476,17 @@ class DistributedGPTQuantizer:
             return hook
 
         handles = [m.register_forward_hook(hook_for(n)) for n, m in layers.items()]
-        seen = ok = 0
+        it = batches if batches is not None else self._model_batches(model, calibration_data)
+        ok = 0
         try:
-            for batch in calibration_data:
-                if seen >= self.quant_config.calibration_samples:
-                    break
-                b = self._inputs(batch)
+            while True:
                 try:
-                    if isinstance(b, dict):
-                        b = {k: v.to(self.device) if torch.is_tensor(v) else v for k, v in b.items()}
-                        rows = next(v for v in b.values() if torch.is_tensor(v)).shape[0]
-                        model(**b)
-                    else:
-                        b = b.to(self.device)
-                        rows = b.shape[0]
-                        model(b)
-                    ok += 1
-                except _HookError:
-                    raise
-                except Exception as e:  # the reference skips a failing batch (:232-236)
-                    logger.warning("error during calibration forward, batch skipped: %s", e)
-                    rows = 0
+                    ran = next(it)
+                except StopIteration:
+                    break
                 finally:
                     hs.end_batch()
-                seen += rows
+                ok += int(ran)
         finally:
             for h in handles:
                 h.remove()
@@ -375,34 +495,20 @@ class DistributedGPTQuantizer:
         return hs
 
     # ---------------------------------------------------------- quantize --
-    def quantize_model(self, model: nn.Module, calibration_data, layers_to_quantize=None,
-                       save_path: Optional[str] = None, progress_callback: Optional[Callable] = None) -> nn.Module:
-        """core/quantizer.py:79-165: calibrate, quantize every layer, optionally
-        save.  ``progress_callback(done, total, name, stats)`` after each
-        layer."""
+    def _quantize_groups(self, model, hs: _SharedHessians, gids: List[int], layers: Dict[str, nn.Linear],
+                         progress: Optional[Callable], counter: List[int]) -> None:
+        """GPTQ on the layers of Hessian groups ``gids`` (largest Hessians
+        first, a few groups per step), each replaced by a QuantizedLinear
+        (``save_packed``) or given its dequantized weights."""
         from .. import pipeline
         from ..models.layers import QuantizedLinear
-        L.require_gpu()
-        t0 = time.time()
-        model.eval()
-        layers = self._resolve_layers(model, layers_to_quantize)
-        if not layers:
-            return model
-        for n, m in layers.items():
-            if m.weight.device.type != "cuda":
-                raise ValueError(f"layer {n} is on {m.weight.device}; move the model to the GPU first")
         cfg = self.quant_config
-        logger.info("found %d layers to quantize", len(layers))
-        hs = self._collect_hessians(model, calibration_data, layers)
         groups = hs.groups()
-        for g, names in groups.items():
+        for g in gids:
             if hs.acc[g].nsamples == 0:
-                raise ValueError(f"layers {names} received no calibration input")
-        # largest Hessians first; a few groups per step bound the memory held
-        # by results
-        order = sorted(groups, key=lambda g: -layers[groups[g][0]].in_features)
-        parents = {n: m for n, m in model.named_modules()}
-        total, done = len(layers), 0
+                raise ValueError(f"layers {groups[g]} received no calibration input")
+        order = sorted(gids, key=lambda g: -layers[groups[g][0]].in_features)
+        parents = dict(model.named_modules())
         for i in range(0, len(order), self.groups_per_step):
             step = order[i:i + self.groups_per_step]
             weights = {n: layers[n].weight.data for g in step for n in groups[g]}
@@ -421,7 +527,7 @@ class DistributedGPTQuantizer:
                         gs = K if cfg.group_size <= 0 or cfg.group_size > K else cfg.group_size
                         q = QuantizedLinear(cfg.bits, gs, K, lin.out_features, bias=lin.bias is not None,
                                             packed=True).to(lin.weight.device)
-                        q.pack_weights(r.codes, r.scale, r.zero, r.g_idx)
+                        q.pack_weights(r.codes, r.scale, r.zero, r.g_idx, perm=r.perm)
                         if lin.bias is not None:
                             q.bias.data = lin.bias.data.clone()
                         parent_name, _, attr = n.rpartition(".")
@@ -433,14 +539,127 @@ class DistributedGPTQuantizer:
                              "nsamples": hs.acc[g].nsamples, "hessian_shared_with": [m for m in groups[g] if m != n]}
                     self.quantized_layers[n] = stats
                     self.quantization_errors[n] = err
-                    done += 1
-                    if progress_callback is not None:
-                        progress_callback(done, total, n, stats)
+                    counter[0] += 1
+                    if progress is not None:
+                        progress(counter[0], counter[1], n, stats)
             del res
+
+    def quantize_model(self, model: nn.Module, calibration_data, layers_to_quantize=None,
+                       save_path: Optional[str] = None, progress_callback: Optional[Callable] = None,
+                       blockwise: Optional[bool] = None) -> nn.Module:
+        """core/quantizer.py:79-165: calibrate, quantize every layer, optionally
+        save.  ``progress_callback(done, total, name, stats)`` after each
+        layer.
+
+        By default, as the reference: one calibration pass over the
+        unquantized model gives every layer's Hessian.  With ``blockwise``
+        (or ``quantization_config.true_sequential``, the reference CLI's
+        --true-sequential, cli.py:207-211) the decoder blocks (the model's
+        largest nn.ModuleList holding the layers) are quantized one at a
+        time, each calibrated on the previous quantized blocks' outputs, and
+        only one block's Hessians are held; with ``true_sequential`` the
+        layer groups inside a block (those fed the same input: q/k/v, then
+        o, gate/up, down) are also calibrated one after another on the
+        outputs of the groups already quantized."""
+        L.require_gpu()
+        t0 = time.time()
+        model.eval()
+        layers = self._resolve_layers(model, layers_to_quantize)
+        if not layers:
+            return model
+        for n, m in layers.items():
+            if m.weight.device.type != "cuda":
+                raise ValueError(f"layer {n} is on {m.weight.device}; move the model to the GPU first")
+        logger.info("found %d layers to quantize", len(layers))
+        counter = [0, len(layers)]
+        seq = self.quant_config.true_sequential
+        blocks = _find_blocks(model, layers) if (blockwise or seq) else None
+        if (blockwise or seq) and blocks is None:
+            logger.warning("no block list holding the layers was found: one calibration pass for all layers")
+        if blocks is None:
+            hs = self._collect_hessians(model, calibration_data, layers)
+            self._quantize_groups(model, hs, list(hs.groups()), layers, progress_callback, counter)
+        else:
+            self._quantize_blockwise(model, calibration_data, layers, blocks, seq, progress_callback, counter)
         self._log_quantization_summary(time.time() - t0)
         if save_path:
             self.save_quantized_model(model, save_path)
         return model
+
+    @torch.no_grad()
+    def _quantize_blockwise(self, model, calibration_data, layers, blocks, true_sequential, progress, counter):
+        prefix, mods = blocks
+        inputs = self._capture_block_inputs(model, calibration_data, mods[0])
+        if not inputs:
+            raise ValueError("no calibration batch reached the first block")
+        cfg_model = getattr(model, "config", None)
+        for i, block in enumerate(mods):
+            mine = {n: m for n, m in layers.items() if n.startswith(f"{prefix}.{i}.")}
+            while mine:
+                def batches(block=block):
+                    for args, kwargs in inputs:
+                        block(*args, **kwargs)
+                        yield True
+                hs = self._collect_hessians(model, None, mine, batches=batches())
+                groups = hs.groups()
+                if true_sequential:
+                    # the group of the first layer the forward reached; the
+                    # other Hessians saw unquantized predecessors: dropped
+                    first = next(n for n in self._call_order if n in mine)
+                    gids = [next(g for g, m in groups.items() if first in m)]
+                else:
+                    gids = list(groups)
+                self._quantize_groups(model, hs, gids, mine, progress, counter)
+                done = {n for g in gids for n in groups[g]}
+                for g in groups:
+                    hs.acc[g].free()
+                mine = {n: m for n, m in mine.items() if n not in done}
+            # this block's outputs (its layers now quantized) feed the next
+            for j, (args, kwargs) in enumerate(inputs):
+                out = block(*args, **kwargs)
+                h = out[0] if isinstance(out, (tuple, list)) else out
+                inputs[j] = ((h,) + tuple(args[1:]), kwargs)
+        rest = {n: m for n, m in layers.items() if not n.startswith(prefix + ".")}
+        if rest:
+            # layers outside the blocks (e.g. a head): one pass over the model,
+            # whose blocks are quantized now
+            hs = self._collect_hessians(model, calibration_data, rest)
+            self._quantize_groups(model, hs, list(hs.groups()), rest, progress, counter)
+        del cfg_model
+
+    def _capture_block_inputs(self, model, calibration_data, first_block) -> List[Tuple[tuple, dict]]:
+        """(args, kwargs) of the first block's call in each calibration
+        forward; the forward stops there.  The model's KV cache is turned off
+        meanwhile (a block is run several times on the same inputs)."""
+        inputs: List[Tuple[tuple, dict]] = []
+
+        def grab(module, args, kwargs):
+            kw = {k: v for k, v in kwargs.items() if k not in ("past_key_value", "past_key_values")}
+            if "use_cache" in kw:
+                kw["use_cache"] = False
+            inputs.append((tuple(args), kw))
+            raise _StopForward
+
+        cfg = getattr(model, "config", None)
+        saved = getattr(cfg, "use_cache", None)
+        if saved is not None:
+            cfg.use_cache = False
+        h = first_block.register_forward_pre_hook(grab, with_kwargs=True)
+        try:
+            for _ in self._model_batches(model, calibration_data):
+                pass
+        finally:
+            h.remove()
+            if saved is not None:
+                cfg.use_cache = saved
+        if inputs and not torch.is_tensor(inputs[0][0][0] if inputs[0][0] else None):
+            # hidden states passed by keyword
+            fixed = []
+            for args, kw in inputs:
+                hs = kw.pop("hidden_states")
+                fixed.append(((hs,) + tuple(args), kw))
+            inputs = fixed
+        return inputs
 
     def _log_quantization_summary(self, elapsed_time: float) -> None:
         total = sum(self.quantization_errors.values())

@@ -139,6 +139,9 @@ struct LinArgs {
   int64_t N, K;
   uint16_t* y;
   int y_dtype;
+  // act-order storage: weight column j holds input column perm[j] (M = 1
+  // gathers x through it; other M get x gathered before the launch)
+  const int32_t* perm;
 };
 
 constexpr int kRB = 4;  // weight rows per wave pass
@@ -355,6 +358,28 @@ __device__ __forceinline__ void load_x_raw(const uint16_t* __restrict__ x, int c
   for (int v = 0; v < 4; ++v) raw[v] = src[v];
 }
 
+// x of one 32-code chunk gathered through perm: raw holds x[perm[32c + t]],
+// t = 0..31, in natural order; indices outside [0, K) are clamped
+__device__ __forceinline__ void load_x_perm(const uint16_t* __restrict__ x, const int32_t* __restrict__ perm,
+                                            int64_t K, int c, u32x4 (&raw)[4]) {
+  typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+  const i32x4* ps = reinterpret_cast<const i32x4*>(perm + static_cast<int64_t>(c) * 32);
+  int idx[32];
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    const i32x4 t = ps[v];
+    idx[4 * v] = t[0]; idx[4 * v + 1] = t[1]; idx[4 * v + 2] = t[2]; idx[4 * v + 3] = t[3];
+  }
+  const int kmax = static_cast<int>(K) - 1;
+  uint32_t h[32];
+#pragma unroll
+  for (int t = 0; t < 32; ++t) h[t] = x[std::min(std::max(idx[t], 0), kmax)];
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) raw[v][w] = h[8 * v + 2 * w] | (h[8 * v + 2 * w + 1] << 16);
+}
+
 // x pairs of one 32-code chunk in pair order, their total X and the magic
 // correction Y = sum_c (off / m_c) X_c
 template <int BITS, bool BF16>
@@ -542,8 +567,13 @@ __global__ __launch_bounds__(256) void gemv_m1_k(LinArgs a) {
     goff[i] = ok ? static_cast<uint32_t>(c / cpg) * 2 : static_cast<uint32_t>(a.ngroups * 2);  // out of range -> 0
   }
   u32x4 xraw[MAXC][4];
+  if (a.perm) {
 #pragma unroll
-  for (int i = 0; i < MAXC; ++i) load_x_raw(a.x, cidx[i], xraw[i]);
+    for (int i = 0; i < MAXC; ++i) load_x_perm(a.x, a.perm, a.K, cidx[i], xraw[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) load_x_raw(a.x, cidx[i], xraw[i]);
+  }
   M1Batch<BITS, MAXC, RB> A, B;
   load_m1_batch<BITS, MAXC, RB>(a, rb * RB, coff, goff, A);
 
@@ -1530,16 +1560,20 @@ int launch_m1_sz(hipStream_t st, const LinArgs& a) {
   return launch_m1_k<BITS, BF16, false>(st, a);
 }
 
+// the M = 1 kernel's layout: buffer descriptors address a row (pitch bytes)
+// and the scale/zero arrays with 31-bit offsets
+bool m1_layout(const LinArgs& a) {
+  const bool bf = a.y_dtype == GPTQ_BF16;
+  return a.M == 1 && a.K % 32 == 0 && a.gs % 32 == 0 && a.K <= 4 * 256 * 32 &&
+         (a.sz_dtype == GPTQ_F16 || (bf && a.sz_dtype == GPTQ_BF16)) && a.N * a.ngroups * 2 <= INT32_MAX &&
+         (reinterpret_cast<uintptr_t>(a.x) % 16) == 0;
+}
+
 template <int BITS, bool BF16>
 int launch_fast(hipStream_t st, const LinArgs& a) {
   using F = Fmt<BITS>;
   const int64_t nch = a.K / F::CB;
-  // buffer descriptors address a row (pitch bytes) and the scale/zero arrays with 31-bit offsets
-  if (a.M == 1 && a.K % 32 == 0 && a.gs % 32 == 0 && a.K <= 4 * 256 * 32 &&
-      (a.sz_dtype == GPTQ_F16 || (BF16 && a.sz_dtype == GPTQ_BF16)) &&
-      a.N * a.ngroups * 2 <= INT32_MAX && (reinterpret_cast<uintptr_t>(a.x) % 16) == 0) {
-    return launch_m1_sz<BITS, BF16>(st, a);
-  }
+  if (m1_layout(a)) return launch_m1_sz<BITS, BF16>(st, a);
   // M = 2..4: the MFMA kernels below (measured 2-3x faster than gemv_k at
   // 28672 x 4096); gemv_k serves the layouts they do not take
   const bool dq_layout = a.K % 128 == 0 && a.gs % 32 == 0;
@@ -1569,10 +1603,26 @@ int launch_fast(hipStream_t st, const LinArgs& a) {
 
 using namespace gptq;
 
-extern "C" int gptq_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packed, int bits, const void* scales,
-                           const void* zeros, int sz_dtype, const int32_t* g_idx, int group_size, int64_t ngroups,
-                           const void* bias, int bias_dtype, int64_t N, int64_t K, void* y, gptq_stream_t stream) {
-  clear_error();
+namespace gptq {
+namespace {
+
+// out[m][j] = x[m][perm[j]] (indices clamped to [0, K))
+__global__ __launch_bounds__(256) void gather_cols_k(const void* __restrict__ x, int esz, int64_t M, int64_t K,
+                                                     const int32_t* __restrict__ perm, void* __restrict__ out) {
+  const int64_t j = blockIdx.x * 256LL + threadIdx.x;
+  if (j >= K) return;
+  const int64_t src = std::min<int64_t>(std::max<int64_t>(perm[j], 0), K - 1);
+  for (int64_t m = blockIdx.y; m < M; m += gridDim.y) {
+    if (esz == 4)
+      static_cast<float*>(out)[m * K + j] = static_cast<const float*>(x)[m * K + src];
+    else
+      static_cast<uint16_t*>(out)[m * K + j] = static_cast<const uint16_t*>(x)[m * K + src];
+  }
+}
+
+int check_linear_args(const void* x, int x_dtype, int64_t M, const uint8_t* packed, int bits, const void* scales,
+                      const void* zeros, int sz_dtype, const int32_t* g_idx, int group_size, int64_t ngroups,
+                      const void* bias, int bias_dtype, int64_t N, int64_t K, void* y) {
   GPTQ_REQUIRE(x && packed && scales && zeros && y, GPTQ_ERR_ARG, "linear: null pointer");
   GPTQ_REQUIRE(bits == 0 || bits == 2 || bits == 3 || bits == 4 || bits == 8, GPTQ_ERR_ARG, "linear: bits=%d", bits);
   GPTQ_REQUIRE(valid_dtype(x_dtype) && valid_dtype(sz_dtype) && (!bias || valid_dtype(bias_dtype)), GPTQ_ERR_DTYPE,
@@ -1581,17 +1631,31 @@ extern "C" int gptq_linear(const void* x, int x_dtype, int64_t M, const uint8_t*
                "linear: bad shape");
   GPTQ_REQUIRE(g_idx || cdiv(K, group_size) <= ngroups, GPTQ_ERR_SHAPE, "linear: too few groups");
   GPTQ_REQUIRE(K <= INT32_MAX / 8, GPTQ_ERR_SHAPE, "linear: K=%lld too large", static_cast<long long>(K));
-  if (M == 0) return GPTQ_OK;
-  hipStream_t st = as_hip(stream);
+  return GPTQ_OK;
+}
+
+LinArgs make_linear_args(const void* x, int x_dtype, int64_t M, const uint8_t* packed, int bits, const void* scales,
+                         const void* zeros, int sz_dtype, int group_size, int64_t ngroups, const void* bias,
+                         int bias_dtype, int64_t N, int64_t K, void* y) {
   const int eb = bits == 0 ? 8 : bits;
   const int64_t pitch = (K * eb + 7) / 8;
-  LinArgs a{static_cast<const uint16_t*>(x), M, packed, pitch, scales, zeros, sz_dtype, group_size, ngroups,
-            bias, bias_dtype, N, K, static_cast<uint16_t*>(y), x_dtype};
-  int cb = eb == 4 ? 32 : eb == 2 ? 64 : eb == 8 ? 16 : 128;
-  const bool fast = x_dtype != GPTQ_F32 && !g_idx && K % cb == 0 && group_size % cb == 0 && K % 32 == 0 &&
-                    (reinterpret_cast<uintptr_t>(packed) % 16) == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0;
-  if (fast) {
-    const bool bf = x_dtype == GPTQ_BF16;
+  return LinArgs{static_cast<const uint16_t*>(x), M, packed, pitch, scales, zeros, sz_dtype, group_size, ngroups,
+                 bias, bias_dtype, N, K, static_cast<uint16_t*>(y), x_dtype, nullptr};
+}
+
+// the fast kernels take 16-bit activations, contiguous groups and chunks of
+// whole 128-bit loads
+bool fast_layout(const LinArgs& a, int bits, const int32_t* g_idx) {
+  const int eb = bits == 0 ? 8 : bits;
+  const int cb = eb == 4 ? 32 : eb == 2 ? 64 : eb == 8 ? 16 : 128;
+  return a.y_dtype != GPTQ_F32 && !g_idx && a.K % cb == 0 && a.gs % cb == 0 && a.K % 32 == 0 &&
+         (reinterpret_cast<uintptr_t>(a.packed) % 16) == 0 && (reinterpret_cast<uintptr_t>(a.x) % 16) == 0;
+}
+
+int dispatch_linear(hipStream_t st, const LinArgs& a, int bits, const int32_t* g_idx) {
+  const int eb = bits == 0 ? 8 : bits;
+  if (fast_layout(a, bits, g_idx)) {
+    const bool bf = a.y_dtype == GPTQ_BF16;
     switch (eb) {
       case 4: return bf ? launch_fast<4, true>(st, a) : launch_fast<4, false>(st, a);
       case 3: return bf ? launch_fast<3, true>(st, a) : launch_fast<3, false>(st, a);
@@ -1599,8 +1663,59 @@ extern "C" int gptq_linear(const void* x, int x_dtype, int64_t M, const uint8_t*
       default: return bf ? launch_fast<8, true>(st, a) : launch_fast<8, false>(st, a);
     }
   }
-  const unsigned blocks = static_cast<unsigned>(cdiv(M * N, 4));
-  hipLaunchKernelGGL(linear_generic, dim3(blocks), dim3(256), 0, st, x, x_dtype, M, packed, bits == 0 ? 0 : bits,
-                     pitch, scales, zeros, sz_dtype, g_idx, group_size, ngroups, bias, bias_dtype, N, K, y);
+  const unsigned blocks = static_cast<unsigned>(cdiv(a.M * a.N, 4));
+  hipLaunchKernelGGL(linear_generic, dim3(blocks), dim3(256), 0, st, static_cast<const void*>(a.x), a.y_dtype, a.M,
+                     a.packed, bits == 0 ? 0 : bits, a.pitch, a.scales, a.zeros, a.sz_dtype, g_idx, a.gs, a.ngroups,
+                     a.bias, a.bias_dtype, a.N, a.K, static_cast<void*>(a.y));
   return check_launch("linear_generic");
+}
+
+}  // namespace
+}  // namespace gptq
+
+using namespace gptq;
+
+extern "C" int gptq_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packed, int bits, const void* scales,
+                           const void* zeros, int sz_dtype, const int32_t* g_idx, int group_size, int64_t ngroups,
+                           const void* bias, int bias_dtype, int64_t N, int64_t K, void* y, gptq_stream_t stream) {
+  clear_error();
+  const int rc = check_linear_args(x, x_dtype, M, packed, bits, scales, zeros, sz_dtype, g_idx, group_size, ngroups,
+                                   bias, bias_dtype, N, K, y);
+  if (rc != GPTQ_OK || M == 0) return rc;
+  const LinArgs a = make_linear_args(x, x_dtype, M, packed, bits, scales, zeros, sz_dtype, group_size, ngroups, bias,
+                                     bias_dtype, N, K, y);
+  return dispatch_linear(as_hip(stream), a, bits, g_idx);
+}
+
+extern "C" size_t gptq_linear_perm_workspace_size(int64_t M, int64_t K, int x_dtype) {
+  if (M <= 0 || K <= 0 || !valid_dtype(x_dtype)) return 0;
+  return static_cast<size_t>(M) * static_cast<size_t>(K) * static_cast<size_t>(dtype_size(x_dtype));
+}
+
+extern "C" int gptq_linear_perm(const void* x, int x_dtype, int64_t M, const int32_t* perm, const uint8_t* packed,
+                                int bits, const void* scales, const void* zeros, int sz_dtype, const int32_t* g_idx,
+                                int group_size, int64_t ngroups, const void* bias, int bias_dtype, int64_t N,
+                                int64_t K, void* y, void* workspace, size_t workspace_bytes, gptq_stream_t stream) {
+  clear_error();
+  GPTQ_REQUIRE(perm, GPTQ_ERR_ARG, "linear_perm: null perm");
+  const int rc = check_linear_args(x, x_dtype, M, packed, bits, scales, zeros, sz_dtype, g_idx, group_size, ngroups,
+                                   bias, bias_dtype, N, K, y);
+  if (rc != GPTQ_OK || M == 0) return rc;
+  hipStream_t st = as_hip(stream);
+  LinArgs a = make_linear_args(x, x_dtype, M, packed, bits, scales, zeros, sz_dtype, group_size, ngroups, bias,
+                               bias_dtype, N, K, y);
+  // M = 1 on the GEMV kernel: x is gathered as the kernel loads it
+  if (fast_layout(a, bits, g_idx) && m1_layout(a) && (reinterpret_cast<uintptr_t>(perm) % 16) == 0) {
+    a.perm = perm;
+    return dispatch_linear(st, a, bits, g_idx);
+  }
+  const size_t need = gptq_linear_perm_workspace_size(M, K, x_dtype);
+  GPTQ_REQUIRE(workspace && workspace_bytes >= need, GPTQ_ERR_WORKSPACE,
+               "linear_perm: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+  const dim3 grid(static_cast<unsigned>(cdiv(K, 256)), static_cast<unsigned>(std::min<int64_t>(M, 65535)));
+  hipLaunchKernelGGL(gather_cols_k, grid, dim3(256), 0, st, x, dtype_size(x_dtype), M, K, perm, workspace);
+  const int lrc = check_launch("gather_cols");
+  if (lrc != GPTQ_OK) return lrc;
+  a.x = static_cast<const uint16_t*>(workspace);
+  return dispatch_linear(st, a, bits, g_idx);
 }

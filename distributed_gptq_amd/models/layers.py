@@ -13,8 +13,16 @@ Buffers keep the reference layout: qweight uint8 (N, ceil(K/2)) for 4-bit
 2/3-bit codes as LSB-first bit streams too (ceil(K*bits/8) bytes per row),
 the layout of the W3A16 GEMV.  ``g_idx[k]`` holds the group of input column
 k (k // group_size unless act-order reordered the groups); the reference's
-placeholder arange(K) (:60, unused by its own unpack) is recognised and read
-as contiguous groups.
+placeholder arange(K) (:60, unused by its own unpack) is read as contiguous
+groups of ``group_size`` (rewritten to arange(K) // group_size when loaded).
+
+One buffer is added: ``perm`` (int32).  Empty, the weight columns are in
+input order.  With act-order (GPTQ's sweep order) it holds K entries and
+weight column j holds input column perm[j], stored so that groups are
+contiguous (g_idx[perm[j]] = j // group_size): the layer is then served by
+the same fast kernels, x gathered through perm, instead of a per-weight
+group lookup.  The operator takes it as an optional last argument, so the
+reference's six-argument call is unchanged.
 """
 from __future__ import annotations
 
@@ -30,8 +38,8 @@ from .. import _ops
 # ------------------------------------------------------------- operator --
 
 _OP_LIB = None
-# id(g_idx) -> (weakref to g_idx, (version, data_ptr), result); tensors
-# cannot be dict keys by value (their == is elementwise)
+# (id(g_idx), id(perm)) -> (weakrefs, stamps, result); tensors cannot be dict
+# keys by value (their == is elementwise)
 _layout_cache: dict = {}
 
 
@@ -47,38 +55,72 @@ def _infer_bits(qweight: torch.Tensor, K: int) -> int:
     raise ValueError(f"qweight rows of {pitch} bytes match no code width for in_features={K}")
 
 
-def _group_layout(g_idx: torch.Tensor, K: int, ngroups: int):
-    """(group_size, g_idx or None): contiguous groups are passed as a group
-    size (fast kernels); anything else as the g_idx gather.  The answer is
-    cached per g_idx tensor and version (one device sync the first time)."""
-    hit = _layout_cache.get(id(g_idx))
-    stamp = (g_idx._version, g_idx.data_ptr())
+def _stamp(t):
+    if t is None:
+        return None
+    # inference tensors have no version counter
+    return (id(t), None if t.is_inference() else t._version, t.data_ptr())
+
+
+def _group_layout(g_idx: torch.Tensor, K: int, ngroups: int, perm: Optional[torch.Tensor] = None):
+    """(group_size, g_idx or None) of the stored weight columns: contiguous
+    groups are passed as a group size (fast kernels), anything else as the
+    per-column group gather (in stored order: g_idx[perm[j]] with perm).
+    The answer is cached per g_idx/perm tensor and version (a few device
+    syncs the first time)."""
+    key = (id(g_idx), id(perm) if perm is not None else 0)
+    stamp = (_stamp(g_idx), _stamp(perm))
+    hit = _layout_cache.get(key)
     if hit is not None and hit[0]() is g_idx and hit[1] == stamp:
         return hit[2]
-    gs = math.ceil(K / ngroups)
     ar = torch.arange(K, device=g_idx.device, dtype=torch.int32)
     gi = g_idx.to(torch.int32)
-    if bool(torch.equal(gi, ar // gs)):
+    if perm is not None:
+        gi = gi[perm.to(device=g_idx.device).long()]
+    if perm is None and ngroups != K and bool(torch.equal(gi, ar)):
+        # the reference's placeholder arange(K): contiguous groups, whose size
+        # only ngroups tells; it is unambiguous when K is a whole number of them
+        gs = math.ceil(K / ngroups)
+        if K % gs:
+            raise ValueError(f"g_idx is the placeholder arange({K}) and {ngroups} groups do not divide K evenly; "
+                             "the group size is ambiguous: pass g_idx = arange(K) // group_size")
         res = (gs, None)
-    elif ngroups != K and bool(torch.equal(gi, ar)):
-        res = (gs, None)  # the reference's placeholder arange(K)
     else:
-        res = (gs, gi.contiguous())
-    key = id(g_idx)
+        gs = int((gi == 0).sum().item())
+        if gs > 0 and math.ceil(K / gs) <= ngroups and bool(torch.equal(gi, ar // gs)):
+            res = (gs, None)
+        else:
+            res = (math.ceil(K / ngroups), gi.contiguous())
     _layout_cache[key] = (weakref.ref(g_idx, lambda _r, k=key: _layout_cache.pop(k, None)), stamp, res)
     return res
 
 
-def _linear_impl(x, qweight, scales, zeros, g_idx, bias):
+def _linear_impl(x, qweight, scales, zeros, g_idx, bias, perm=None):
     K = g_idx.numel()
     bits = _infer_bits(qweight, K)
-    gs, gi = _group_layout(g_idx, K, scales.shape[1])
-    return _ops.linear(x, qweight, bits, scales, zeros, K, g_idx=gi, group_size=gs, bias=bias)
+    if perm is not None and perm.numel() == 0:
+        perm = None
+    gs, gi = _group_layout(g_idx, K, scales.shape[1], perm)
+    return _ops.linear(x, qweight, bits, scales, zeros, K, g_idx=gi, group_size=gs, bias=bias, perm=perm)
+
+
+def _dequant_input_order(qweight, scales, zeros, g_idx, perm=None) -> torch.Tensor:
+    """fp32 (N, K) dequantised weights in input-column order."""
+    K = g_idx.numel()
+    if perm is not None and perm.numel() == 0:
+        perm = None
+    gs, gi = _group_layout(g_idx, K, scales.shape[1], perm)
+    W = _ops.dequant(qweight, _infer_bits(qweight, K), scales, zeros, K, g_idx=gi, group_size=gs)
+    if perm is None:
+        return W
+    out = torch.empty_like(W)
+    out[:, perm.long()] = W
+    return out
 
 
 def _linear_setup(ctx, inputs, output):
-    x, qweight, scales, zeros, g_idx, bias = inputs
-    ctx.save_for_backward(qweight, scales, zeros, g_idx)
+    x, qweight, scales, zeros, g_idx, bias, perm = inputs
+    ctx.save_for_backward(qweight, scales, zeros, g_idx, perm)
     ctx.x_dtype = x.dtype
     ctx.has_bias = bias is not None
 
@@ -86,16 +128,14 @@ def _linear_setup(ctx, inputs, output):
 def _linear_backward(ctx, grad):
     """Gradients of the fallback F.linear(x, unpack_weights(), bias): the
     quantized weights are constants; x and bias get their usual gradients."""
-    qweight, scales, zeros, g_idx = ctx.saved_tensors
+    qweight, scales, zeros, g_idx, perm = ctx.saved_tensors
     gx = gb = None
     if ctx.needs_input_grad[0]:
-        K = g_idx.numel()
-        gs, gi = _group_layout(g_idx, K, scales.shape[1])
-        W = _ops.dequant(qweight, _infer_bits(qweight, K), scales, zeros, K, g_idx=gi, group_size=gs)
+        W = _dequant_input_order(qweight, scales, zeros, g_idx, perm)
         gx = (grad.float() @ W).to(ctx.x_dtype)
     if ctx.has_bias and ctx.needs_input_grad[5]:
         gb = grad.reshape(-1, grad.shape[-1]).float().sum(0)
-    return gx, None, None, None, None, gb
+    return gx, None, None, None, None, gb, None
 
 
 def register_ops():
@@ -106,7 +146,8 @@ def register_ops():
     if hasattr(torch.ops, "gptq") and hasattr(torch.ops.gptq, "linear"):
         return
     lib = torch.library.Library("gptq", "DEF")
-    lib.define("linear(Tensor x, Tensor qweight, Tensor scales, Tensor zeros, Tensor g_idx, Tensor? bias) -> Tensor")
+    lib.define("linear(Tensor x, Tensor qweight, Tensor scales, Tensor zeros, Tensor g_idx, Tensor? bias, "
+               "Tensor? perm=None) -> Tensor")
     lib.impl("linear", _linear_impl, "CUDA")
     torch.library.register_autograd("gptq::linear", _linear_backward, setup_context=_linear_setup, lib=lib)
     _OP_LIB = lib
@@ -137,31 +178,74 @@ class QuantizedLinear(nn.Module):
         self.register_buffer("scales", torch.zeros((out_features, self.num_groups), dtype=torch.float16))
         self.register_buffer("zeros", torch.zeros((out_features, self.num_groups), dtype=torch.float16))
         self.register_buffer("g_idx", torch.arange(in_features, dtype=torch.int32) // self.group_size)
+        self.register_buffer("perm", torch.zeros(0, dtype=torch.int32))
         if bias:
             self.register_parameter("bias", nn.Parameter(torch.zeros(out_features)))
         else:
             self.register_parameter("bias", None)
 
     def pack_weights(self, weight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor,
-                     g_idx: Optional[torch.Tensor] = None):
-        """Store integer codes (N, K) and fp16 scales/zeros (:67-96)."""
+                     g_idx: Optional[torch.Tensor] = None, perm: Optional[torch.Tensor] = None):
+        """Store integer codes (N, K, input-column order) and fp16
+        scales/zeros (:67-96).  With an act-order ``g_idx`` (groups out of
+        input order) the columns are stored in ``perm`` order, the order
+        that makes the groups contiguous (given, or the stable sort of
+        g_idx); ``g_idx`` itself keeps its meaning (group of input column k)."""
         codes = weight.to(torch.uint8)
-        self.qweight.data = _ops.pack(codes, self.bits) if self.packed else codes.contiguous()
+        dev = codes.device
         self.scales.data = scales.to(torch.float16).reshape(self.out_features, -1).contiguous()
         self.zeros.data = zeros.to(torch.float16).reshape(self.out_features, -1).contiguous()
         if g_idx is not None:
-            self.g_idx.data = g_idx.to(torch.int32).to(self.qweight.device)
+            self.g_idx.data = g_idx.to(torch.int32).to(dev)
+        ar = torch.arange(self.in_features, dtype=torch.int32, device=dev)
+        gi = self.g_idx.to(dev)
+        if perm is None and not bool(torch.equal(gi, ar // self.group_size)):
+            cand = torch.argsort(gi, stable=True).to(torch.int32)
+            if bool(torch.equal(gi[cand.long()], ar // self.group_size)):
+                perm = cand
+        if perm is not None:
+            perm = perm.to(device=dev, dtype=torch.int32)
+            if bool(torch.equal(perm, ar)):
+                perm = None
+        if perm is not None:
+            codes = codes[:, perm.long()]
+            self.perm.data = perm.contiguous()
+        else:
+            self.perm.data = torch.zeros(0, dtype=torch.int32, device=dev)
+        self.qweight.data = _ops.pack(codes, self.bits) if self.packed else codes.contiguous()
 
     def unpack_weights(self) -> torch.Tensor:
-        """fp32 (N, K) = (q - zero) * scale per group (:98-138), bit-exact."""
-        bits = self.bits if self.packed else 0
-        gs, gi = _group_layout(self.g_idx, self.in_features, self.num_groups)
-        return _ops.dequant(self.qweight, bits, self.scales, self.zeros, self.in_features, g_idx=gi,
-                            group_size=gs)
+        """fp32 (N, K) = (q - zero) * scale per group (:98-138), bit-exact,
+        in input-column order."""
+        return _dequant_input_order(self.qweight, self.scales, self.zeros, self.g_idx, self.perm)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """:140-157 -- the gptq::linear operator, registered above."""
+        if self.perm.numel():
+            return torch.ops.gptq.linear(x, self.qweight, self.scales, self.zeros, self.g_idx, self.bias, self.perm)
         return torch.ops.gptq.linear(x, self.qweight, self.scales, self.zeros, self.g_idx, self.bias)
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
+                              error_msgs):
+        # perm has K entries with act-order and none otherwise; the
+        # reference's checkpoints have no perm at all (identity)
+        key = prefix + "perm"
+        saved = state_dict.get(key)
+        if saved is not None and saved.shape != self.perm.shape:
+            self.perm.data = torch.empty(saved.shape, dtype=torch.int32, device=self.perm.device)
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
+                                      error_msgs)
+        if saved is None:
+            if key in missing_keys:
+                missing_keys.remove(key)
+            self.perm.data = torch.zeros(0, dtype=torch.int32, device=self.perm.device)
+        # the reference's placeholder g_idx = arange(K) (models/layers.py:60)
+        # means contiguous groups of group_size
+        K = self.in_features
+        if self.num_groups != K and self.g_idx.numel() == K and not self.perm.numel():
+            ar = torch.arange(K, dtype=torch.int32, device=self.g_idx.device)
+            if bool(torch.equal(self.g_idx.to(torch.int32), ar)):
+                self.g_idx.data = ar // self.group_size
 
     @classmethod
     def from_linear(cls, linear_layer: nn.Linear, bits: int = 4, group_size: int = 128,
@@ -184,7 +268,7 @@ class QuantizedLinear(nn.Module):
         q = cls(bits=gptq.bits, group_size=gs if gs > 0 else layer.in_features, in_features=layer.in_features,
                 out_features=layer.out_features, bias=layer.bias is not None, packed=packed)
         q = q.to(layer.weight.device)
-        q.pack_weights(gptq.qcodes, gptq.scale, gptq.zero, gptq.g_idx)
+        q.pack_weights(gptq.qcodes, gptq.scale, gptq.zero, gptq.g_idx, perm=gptq.perm)
         if layer.bias is not None:
             q.bias.data = layer.bias.data.clone()
         return q

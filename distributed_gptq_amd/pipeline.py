@@ -36,6 +36,7 @@ class LayerResult:
     g_idx: torch.Tensor        # (K,) int32: group of input column k
     dequant: Optional[torch.Tensor]  # (N, K) layer dtype
     losses_sum: torch.Tensor   # () fp32 device scalar
+    perm: Optional[torch.Tensor] = None  # (K,) int32 sweep order with act-order, else None
 
 
 def factorize(H: torch.Tensor, nsamples: int, percdamp: float, actorder: bool):
@@ -87,7 +88,8 @@ def _quantize_one(W, U, perm, dead, bits, group_size, blocksize, want_dequant) -
         g_idx = torch.empty_like(ar)
         g_idx[perm.long()] = gcol
     return LayerResult(codes=res["codes"], qweight=_ops.pack(res["codes"], bits), scale=res["scale"],
-                       zero=res["zero"], g_idx=g_idx, dequant=res["dequant"], losses_sum=0.5 * res["err_sq"].sum())
+                       zero=res["zero"], g_idx=g_idx, dequant=res["dequant"], losses_sum=0.5 * res["err_sq"].sum(),
+                       perm=perm)
 
 
 class PendingLayers:

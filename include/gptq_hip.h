@@ -209,6 +209,25 @@ int gptq_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packed,
                 const void* bias, int bias_dtype, int64_t N, int64_t K,
                 void* y, gptq_stream_t stream);
 
+/* y = x[:, perm] @ W^T (+ bias), W and the other arguments as in
+ * gptq_linear: the act-order serving layout, where weight column j holds
+ * input column perm[j] (perm: K int32, a permutation of [0, K); entries
+ * outside [0, K) are clamped) so that groups are contiguous in the stored
+ * order and the fast kernels serve the layer.  With M = 1 and a layout the
+ * GEMV takes, x is gathered inside the kernel; otherwise the gathered x
+ * (gptq_linear_perm_workspace_size bytes) is written to the workspace first.
+ * Replaces torch.ops.gptq.linear (models/layers.py:151-153) for GPTQ
+ * act-order output, whose g_idx (:60) maps input columns to groups out of
+ * order; semantics F.linear(x, unpack_weights(), bias) (:155-157). */
+size_t gptq_linear_perm_workspace_size(int64_t M, int64_t K, int x_dtype);
+int gptq_linear_perm(const void* x, int x_dtype, int64_t M, const int32_t* perm,
+                     const uint8_t* packed, int bits, const void* scales,
+                     const void* zeros, int sz_dtype, const int32_t* g_idx,
+                     int group_size, int64_t ngroups, const void* bias,
+                     int bias_dtype, int64_t N, int64_t K, void* y,
+                     void* workspace, size_t workspace_bytes,
+                     gptq_stream_t stream);
+
 /* ------------------------------------------------- elementwise quantise --
  * Flat groups of group_size consecutive elements (the tensor API of
  * kernels/triton_kernels.py:377-481): per group s = (max - min) / maxq,

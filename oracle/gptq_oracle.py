@@ -228,7 +228,7 @@ def gptq_ref(weight, Hinv, bits, group_size, blocksize):
 
 
 def gptq_canonical(weight, H_raw, nsamples, bits, group_size, blocksize,
-                   percdamp, actorder=False, dtype=np.float64, U=None):
+                   percdamp, actorder=False, dtype=np.float64, U=None, perm=None):
     """Canonical GPTQ (paper Alg. 1, ``fasterquant``) on weight (N, K).
 
     group_size = -1 means one group per row (per-channel).  Group parameters
@@ -238,7 +238,10 @@ def gptq_canonical(weight, H_raw, nsamples, bits, group_size, blocksize,
     decreasing H_ii and groups are contiguous in that order.
 
     If ``U`` is given it is used as the upper Cholesky factor of the damped,
-    permuted H^-1 instead of computing it (so a GPU factor can be fed in).
+    permuted H^-1 instead of computing it (so a GPU factor can be fed in);
+    ``perm`` then gives the act-order permutation that factor belongs to
+    (when diagonal entries nearly tie, the order computed here in ``dtype``
+    can differ from the one the factor was built for).
 
     Returns dict(codes (N, K) in original column order, scale/zero
     (N, ngroups), g_idx (K,), perm (K,), dequant (N, K), losses (N, K),
@@ -247,20 +250,33 @@ def gptq_canonical(weight, H_raw, nsamples, bits, group_size, blocksize,
     W = np.array(weight, dtype=dtype, copy=True)
     rows, cols = W.shape
     maxq = 2 ** bits - 1
-    H, dead = prepare_canonical_H(np.asarray(H_raw, dtype=dtype), nsamples, 0.0)
+    if U is None:
+        H, dead = prepare_canonical_H(np.asarray(H_raw, dtype=dtype), nsamples, 0.0)
+        diag = np.diag(H)
+    else:
+        # a given factor needs only the diagonal (dead columns, act-order):
+        # the same values prepare_canonical_H puts there, without K x K work
+        diag = (2.0 / nsamples) * np.asarray(np.diag(H_raw), dtype=dtype)
+        dead = diag == 0
+        diag = np.where(dead, dtype(1), diag)
     # damping is applied after the permutation, on the permuted matrix;
     # mean(diag) is permutation invariant so the order does not matter
     if group_size == -1:
         s_pc, z_pc = canonical_params(W, maxq)
     W[:, dead] = 0
-    perm = np.arange(cols)
+    if actorder and perm is not None:
+        perm = np.asarray(perm, dtype=np.int64)
+    elif actorder:
+        perm = np.argsort(-diag, kind="stable")
+    else:
+        perm = np.arange(cols)
     if actorder:
-        perm = np.argsort(-np.diag(H), kind="stable")
         W = W[:, perm]
-        H = H[perm][:, perm]
-    H = H.copy()
-    H[np.diag_indices_from(H)] += percdamp * np.mean(np.diag(H))
     if U is None:
+        if actorder:
+            H = H[perm][:, perm]
+        H = H.copy()
+        H[np.diag_indices_from(H)] += percdamp * np.mean(np.diag(H))
         U = upper_chol_of_inverse(H)
     U = np.asarray(U, dtype=dtype)
     gs = cols if group_size == -1 else group_size
@@ -300,6 +316,87 @@ def gptq_canonical(weight, H_raw, nsamples, bits, group_size, blocksize,
     return dict(codes=Q[:, invperm], dequant=Qv[:, invperm], scale=scale,
                 zero=zero, g_idx=g_idx, perm=perm, losses=Losses[:, invperm],
                 U=U)
+
+
+def code_margin(y, q, maxq):
+    """How far y = w / s + z lies outside the cell of values whose canonical
+    code clamp(round(w / s) + z, 0, maxq) is q (z integral), in quantisation
+    steps: 0 inside [q - 1/2, q + 1/2], the cell being open-ended at code 0
+    and at maxq."""
+    lo = np.where(q <= 0, -np.inf, q - 0.5)
+    hi = np.where(q >= maxq, np.inf, q + 0.5)
+    return np.maximum(np.maximum(lo - y, y - hi), 0.0)
+
+
+def gptq_canonical_replay(weight, U, perm, dead, bits, group_size, blocksize, codes, scale, zero):
+    """fp64 replay of the canonical sweep along given decisions.
+
+    Runs ``gptq_canonical``'s loop (same order, same lazy-batch updates) with
+    the factor ``U`` (sweep order), but takes the codes and the group
+    parameters from ``codes`` (N x K, original column order) and
+    ``scale``/``zero`` (N x ngroups, sweep group order) instead of deciding
+    them, so one different decision cannot cascade.  Returns
+
+    * ``margin`` (N x K, original order): per weight, how far the replayed
+      w / s + z lies outside the rounding cell of the given code, in
+      quantisation steps (0 = the given code is the correct rounding of the
+      fp64 value along that trajectory);
+    * ``scale``/``zero``: the group parameters the replay computes itself at
+      each group start (per-channel: from the original weight), and
+      ``zero_margin``: the distance of -xmin / s from the nearest rounding
+      tie (a zero point within a hair of a tie may legitimately differ).
+    """
+    W = np.array(weight, dtype=np.float64, copy=True)
+    rows, cols = W.shape
+    maxq = 2 ** bits - 1
+    perm = np.arange(cols) if perm is None else np.asarray(perm)
+    dead = np.zeros(cols, bool) if dead is None else np.asarray(dead, bool)
+    gs = cols if group_size == -1 else group_size
+    ngroups = (cols + gs - 1) // gs
+    s_own = np.zeros((rows, ngroups))
+    z_own = np.zeros((rows, ngroups))
+    z_tie = np.full((rows, ngroups), np.inf)
+
+    def own_params(x, g):
+        xmin = np.minimum(x.min(axis=1), 0.0)
+        xmax = np.maximum(x.max(axis=1), 0.0)
+        both0 = (xmin == 0) & (xmax == 0)
+        xmin = np.where(both0, -1.0, xmin)
+        xmax = np.where(both0, 1.0, xmax)
+        s = (xmax - xmin) / maxq
+        v = -xmin / s
+        s_own[:, g], z_own[:, g] = s, np.round(v)
+        z_tie[:, g] = np.abs(np.abs(v - np.floor(v)) - 0.5)
+
+    if group_size == -1:
+        own_params(W, 0)
+    W[:, dead] = 0
+    W = W[:, perm]
+    Q = np.asarray(codes, np.float64)[:, perm]
+    S = np.asarray(scale, np.float64)
+    Z = np.asarray(zero, np.float64)
+    U = np.asarray(U, np.float64)
+    margin = np.zeros_like(W)
+    for i1 in range(0, cols, blocksize):
+        i2 = min(i1 + blocksize, cols)
+        if group_size != -1:
+            for c in range(i1, i2):
+                if c % gs == 0:
+                    own_params(W[:, c:min(c + gs, cols)], c // gs)
+        W1 = W[:, i1:i2].copy()
+        Err1 = np.zeros_like(W1)
+        for j in range(i2 - i1):
+            c = i1 + j
+            s, z = S[:, c // gs], Z[:, c // gs]
+            w = W1[:, j]
+            q = Q[:, c]
+            margin[:, c] = code_margin(w / s + z, q, maxq)
+            e = (w - s * (q - z)) / U[c, c]
+            W1[:, j:] -= np.outer(e, U[c, c:i2])
+            Err1[:, j] = e
+        W[:, i2:] -= Err1 @ U[i1:i2, i2:]
+    inv = np.argsort(perm)
+    return dict(margin=margin[:, inv], scale=s_own, zero=z_own, zero_margin=z_tie)
 
 
 def obs_bruteforce(weight, Hd, bits, group_size, param_snapshot_cols=None):

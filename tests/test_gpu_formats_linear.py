@@ -271,3 +271,168 @@ def test_linear_scales_at_odd_offset(hip, xdt, M, N):
     y_al = _ops.linear(xc, packed, bits, s_al, z_al, K, group_size=gs)
     y_odd = _ops.linear(xc, packed, bits, s_odd, z_odd, K, group_size=gs)
     assert torch.equal(y_al, y_odd)
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+@pytest.mark.parametrize("gs", [128, 32])
+@pytest.mark.parametrize("M,N", [(2, 8192 + 37), (4, 8192 + 37), (16, 8192 + 37),
+                                 (2, 16384 + 5), (4, 16384 + 5), (16, 16384 + 5)])
+def test_linear_small_m_wide_n(hip, xdt, bits, gs, M, N):
+    """M <= 16 with N >= 8192 and >= 16384: the 64-row register kernels
+    (3/4-bit: dq_reg4_k with 8 and 4 waves) and the wide split-K kernels
+    (2/8-bit), ragged N (the last tile's clamp), with groups of 128 (zero
+    points folded per block) and 32 (dequantised per weight)."""
+    from distributed_gptq_amd import _ops
+    K = 1024
+    codes, scales, zeros, x = _case(M, N, K, bits, gs, M + N + bits + gs, xdt)
+    bias = torch.randn(N).to(xdt)
+    packed = torch.from_numpy(O.pack_bitstream(codes, bits)).cuda()
+    y = _ops.linear(x.cuda(), packed, bits, scales.cuda(), zeros.cuda(), K, group_size=gs, bias=bias.cuda())
+    ref = O.linear(x.float().numpy(), codes, scales.numpy(), zeros.numpy(), np.arange(K) // gs, bias.float().numpy())
+    err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err < TOL[xdt], err
+
+
+_C4 = {}
+
+
+def _c4_weights(N, K, bits):
+    """Config 4's weights (codes uniform, scales U(1e-3, 1e-2), zeros
+    2^(bits-1), fp16) and their oracle dequantisation, one shape cached."""
+    key = (N, K, bits)
+    if key not in _C4:
+        _C4.clear()
+        rng = np.random.default_rng(3)
+        codes = rng.integers(0, 2 ** bits, (N, K)).astype(np.uint8)
+        ng = K // 128
+        scales = torch.from_numpy(rng.uniform(1e-3, 1e-2, (N, ng))).half()
+        zeros = torch.full((N, ng), float(2 ** (bits - 1))).half()
+        Wd = O.dequant(codes, scales.numpy(), zeros.numpy(), np.arange(K) // 128).astype(np.float64)
+        packed = torch.from_numpy(O.pack_bitstream(codes, bits)).cuda()
+        _C4[key] = (packed, scales.cuda(), zeros.cuda(), Wd)
+    return _C4[key]
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M", [1, 16, 128])
+@pytest.mark.parametrize("bits", [3, 4])
+@pytest.mark.parametrize("N,K", [(4096, 4096), (14336, 4096), (4096, 14336), (28672, 4096)])
+def test_linear_config4_shapes(hip, xdt, M, bits, N, K):
+    """Every kernel the bench's W4A16 / W3A16 rows run, at their shapes."""
+    from distributed_gptq_amd import _ops
+    packed, scales, zeros, Wd = _c4_weights(N, K, bits)
+    g = torch.Generator().manual_seed(M + bits)
+    x = torch.randn(M, K, generator=g).to(xdt)
+    y = _ops.linear(x.cuda(), packed, bits, scales, zeros, K, group_size=128)
+    ref = x.double().numpy() @ Wd.T
+    err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err < TOL[xdt], err
+
+
+def test_release_config4_cache(hip):
+    _C4.clear()
+
+
+# ------------------------------------------------ act-order serving layout --
+
+def _actorder_case(M, N, K, bits, gs, seed, xdt):
+    """Codes in input-column order with an act-order g_idx (groups of gs in a
+    random column order), and the storage the serving layout uses: columns
+    in perm order, perm = the stable sort of g_idx."""
+    codes, scales, zeros, x = _case(M, N, K, bits, gs, seed, xdt)
+    rng = np.random.default_rng(seed + 1)
+    perm = rng.permutation(K).astype(np.int32)          # sweep order
+    g_idx = np.empty(K, np.int32)
+    g_idx[perm] = np.arange(K) // gs                    # group of input column k
+    stored = codes[:, perm]
+    return codes, stored, scales, zeros, x, g_idx, perm
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bits", [3, 4, 8])
+@pytest.mark.parametrize("M,N,K", [(1, 1000, 4096), (1, 37, 14336), (2, 8229, 1024), (16, 4101, 4096),
+                                   (16, 16389, 1024), (128, 4096, 4096), (40, 1000, 1024)])
+def test_linear_perm_matches_oracle(hip, xdt, bits, M, N, K):
+    """gptq_linear_perm: the M = 1 GEMV with x gathered in the kernel, other
+    M on the fast kernels after the gather; against the oracle on the
+    input-order codes and act-order g_idx, at the fast path's tolerance."""
+    from distributed_gptq_amd import _ops
+    gs = 128
+    codes, stored, scales, zeros, x, g_idx, perm = _actorder_case(M, N, K, bits, gs, M + N + bits, xdt)
+    bias = torch.randn(N).to(xdt)
+    packed = torch.from_numpy(O.pack_bitstream(stored, bits)).cuda()
+    y = _ops.linear(x.cuda(), packed, bits, scales.cuda(), zeros.cuda(), K, group_size=gs, bias=bias.cuda(),
+                    perm=torch.from_numpy(perm).cuda())
+    ref = O.linear(x.float().numpy(), codes, scales.numpy(), zeros.numpy(), g_idx, bias.float().numpy())
+    err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err < TOL[xdt], err
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
+def test_linear_perm_generic_and_fp32(hip, xdt):
+    """perm with layouts the fast kernels do not take (fp32 x; a g_idx that
+    stays out of order in the stored order): gather, then the generic
+    kernel."""
+    from distributed_gptq_amd import _ops
+    N, K, gs = 40, 200, 50
+    codes, scales, zeros, x = _case(5, N, K, 4, gs, 3, xdt)
+    rng = np.random.default_rng(1)
+    perm = rng.permutation(K).astype(np.int32)
+    g_idx = rng.permutation(np.arange(K) // gs).astype(np.int32)   # group of input column k
+    stored = codes[:, perm]
+    packed = torch.from_numpy(O.pack_bitstream(stored, 4)).cuda()
+    y = _ops.linear(x.cuda(), packed, 4, scales.cuda(), zeros.cuda(), K,
+                    g_idx=torch.from_numpy(g_idx[perm]).cuda(), perm=torch.from_numpy(perm).cuda())
+    ref = O.linear(x.float().numpy(), codes, scales.numpy(), zeros.numpy(), g_idx)
+    err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err < TOL[xdt] * 10, err
+
+
+@pytest.mark.parametrize("bits,gs,M", [(4, 128, 1), (4, 128, 7), (3, 64, 1), (8, 128, 16), (2, 32, 1)])
+def test_quantized_linear_actorder_is_served_fast(hip, bits, gs, M):
+    """GPTQ act-order output in a QuantizedLinear: stored in sweep order with
+    perm, the operator takes the contiguous-group kernels (no per-weight
+    group gather), outputs match the oracle on the input-order codes, the
+    dequantised weight equals the layer's, gradients flow, and the state
+    dict round-trips (a model without perm loads too)."""
+    from distributed_gptq_amd import GPTQ
+    from distributed_gptq_amd.models import layers as Lm
+    torch.manual_seed(bits + gs)
+    K, N = 512, 96
+    lin = torch.nn.Linear(K, N).cuda().half()
+    X = torch.randn(2, 128, K, device="cuda").half()
+    X[..., :5] *= 10
+    q = GPTQ(lin, bits=bits, group_size=gs, actorder=True, device="cuda")
+    q.add_batch(X)
+    q.fasterquant()
+    ql = Lm.QuantizedLinear.from_gptq(q)
+    assert ql.perm.numel() == K and torch.equal(ql.perm, q.perm)
+    assert Lm._group_layout(ql.g_idx, K, ql.num_groups, ql.perm) == (gs, None)
+    Wd = ql.unpack_weights()
+    np.testing.assert_array_equal(Wd.cpu().numpy(), O.dequant(
+        q.qcodes.cpu().numpy(), ql.scales.cpu().numpy(), ql.zeros.cpu().numpy(), q.g_idx.cpu().numpy()))
+    x = torch.randn(M, K, device="cuda").half()
+    with torch.no_grad():
+        y = ql(x)
+    ref = O.linear(x.float().cpu().numpy(), q.qcodes.cpu().numpy(), ql.scales.cpu().numpy(),
+                   ql.zeros.cpu().numpy(), q.g_idx.cpu().numpy(), ql.bias.detach().float().cpu().numpy())
+    err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err < TOL[torch.float16], err
+    # gradients of F.linear(x, unpack_weights(), bias)
+    xg = x.float().requires_grad_(True)
+    out = ql(xg)
+    out.backward(torch.ones_like(out))
+    np.testing.assert_allclose(xg.grad.cpu().numpy(), np.tile(Wd.sum(0).cpu().numpy(), (M, 1)), rtol=1e-4,
+                               atol=1e-5)
+    # state dict round trip into a fresh layer, and a perm-less (reference) one
+    fresh = Lm.QuantizedLinear(bits, gs, K, N, bias=True, packed=True).cuda()
+    fresh.load_state_dict(ql.state_dict())
+    with torch.no_grad():
+        assert torch.equal(fresh(x), y)
+    plain = Lm.QuantizedLinear.from_gptq(q)
+    plain.pack_weights(q.qcodes, q.scale, q.zero, torch.arange(K, device="cuda") // gs)
+    assert plain.perm.numel() == 0
+    sd = {k: v for k, v in plain.state_dict().items() if k != "perm"}
+    fresh.load_state_dict(sd)
+    assert fresh.perm.numel() == 0 and torch.equal(fresh.qweight, plain.qweight)

@@ -40,7 +40,7 @@ def _run(lin, X, **kw):
     (80, 256, 8, -1, 128, False),     # per-channel
     (64, 512, 4, 128, 256, False),    # blocksize > 128 (two sub-blocks per block)
     (33, 160, 4, 32, 96, True),
-    (40, 256, 4, 8, 128, False),      # 16 groups per sub-block: the lanes-own-columns kernel
+    (40, 256, 4, 8, 128, False),      # 16 groups per sub-block (group parameters of 8-column groups)
     (130, 320, 4, 64, 128, True),     # rows beyond one 128-row workgroup
 ])
 def test_fasterquant_matches_oracle(hip, N, K, bits, gs, bs, actorder):
