@@ -139,9 +139,6 @@ struct LinArgs {
   int64_t N, K;
   uint16_t* y;
   int y_dtype;
-  // act-order storage: weight column j holds input column perm[j] (M = 1
-  // gathers x through it; other M get x gathered before the launch)
-  const int32_t* perm;
 };
 
 constexpr int kRB = 4;  // weight rows per wave pass
@@ -358,28 +355,6 @@ __device__ __forceinline__ void load_x_raw(const uint16_t* __restrict__ x, int c
   for (int v = 0; v < 4; ++v) raw[v] = src[v];
 }
 
-// x of one 32-code chunk gathered through perm: raw holds x[perm[32c + t]],
-// t = 0..31, in natural order; indices outside [0, K) are clamped
-__device__ __forceinline__ void load_x_perm(const uint16_t* __restrict__ x, const int32_t* __restrict__ perm,
-                                            int64_t K, int c, u32x4 (&raw)[4]) {
-  typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-  const i32x4* ps = reinterpret_cast<const i32x4*>(perm + static_cast<int64_t>(c) * 32);
-  int idx[32];
-#pragma unroll
-  for (int v = 0; v < 8; ++v) {
-    const i32x4 t = ps[v];
-    idx[4 * v] = t[0]; idx[4 * v + 1] = t[1]; idx[4 * v + 2] = t[2]; idx[4 * v + 3] = t[3];
-  }
-  const int kmax = static_cast<int>(K) - 1;
-  uint32_t h[32];
-#pragma unroll
-  for (int t = 0; t < 32; ++t) h[t] = x[std::min(std::max(idx[t], 0), kmax)];
-#pragma unroll
-  for (int v = 0; v < 4; ++v)
-#pragma unroll
-    for (int w = 0; w < 4; ++w) raw[v][w] = h[8 * v + 2 * w] | (h[8 * v + 2 * w + 1] << 16);
-}
-
 // x pairs of one 32-code chunk in pair order, their total X and the magic
 // correction Y = sum_c (off / m_c) X_c
 template <int BITS, bool BF16>
@@ -567,13 +542,8 @@ __global__ __launch_bounds__(256) void gemv_m1_k(LinArgs a) {
     goff[i] = ok ? static_cast<uint32_t>(c / cpg) * 2 : static_cast<uint32_t>(a.ngroups * 2);  // out of range -> 0
   }
   u32x4 xraw[MAXC][4];
-  if (a.perm) {
 #pragma unroll
-    for (int i = 0; i < MAXC; ++i) load_x_perm(a.x, a.perm, a.K, cidx[i], xraw[i]);
-  } else {
-#pragma unroll
-    for (int i = 0; i < MAXC; ++i) load_x_raw(a.x, cidx[i], xraw[i]);
-  }
+  for (int i = 0; i < MAXC; ++i) load_x_raw(a.x, cidx[i], xraw[i]);
   M1Batch<BITS, MAXC, RB> A, B;
   load_m1_batch<BITS, MAXC, RB>(a, rb * RB, coff, goff, A);
 
@@ -1640,7 +1610,7 @@ LinArgs make_linear_args(const void* x, int x_dtype, int64_t M, const uint8_t* p
   const int eb = bits == 0 ? 8 : bits;
   const int64_t pitch = (K * eb + 7) / 8;
   return LinArgs{static_cast<const uint16_t*>(x), M, packed, pitch, scales, zeros, sz_dtype, group_size, ngroups,
-                 bias, bias_dtype, N, K, static_cast<uint16_t*>(y), x_dtype, nullptr};
+                 bias, bias_dtype, N, K, static_cast<uint16_t*>(y), x_dtype};
 }
 
 // the fast kernels take 16-bit activations, contiguous groups and chunks of
@@ -1704,11 +1674,10 @@ extern "C" int gptq_linear_perm(const void* x, int x_dtype, int64_t M, const int
   hipStream_t st = as_hip(stream);
   LinArgs a = make_linear_args(x, x_dtype, M, packed, bits, scales, zeros, sz_dtype, group_size, ngroups, bias,
                                bias_dtype, N, K, y);
-  // M = 1 on the GEMV kernel: x is gathered as the kernel loads it
-  if (fast_layout(a, bits, g_idx) && m1_layout(a) && (reinterpret_cast<uintptr_t>(perm) % 16) == 0) {
-    a.perm = perm;
-    return dispatch_linear(st, a, bits, g_idx);
-  }
+  // x is gathered once, before the launch, for every M: inside the kernels
+  // each wave would gather all of x with scattered loads, and one 16-bit load
+  // per lane touches 64 cache lines (M = 1 at 4096 x 4096 measured 13.4 us
+  // that way against 4.8 us for the GEMV alone)
   const size_t need = gptq_linear_perm_workspace_size(M, K, x_dtype);
   GPTQ_REQUIRE(workspace && workspace_bytes >= need, GPTQ_ERR_WORKSPACE,
                "linear_perm: workspace of %zu bytes, %zu needed", workspace_bytes, need);

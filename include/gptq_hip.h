@@ -213,9 +213,9 @@ int gptq_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packed,
  * gptq_linear: the act-order serving layout, where weight column j holds
  * input column perm[j] (perm: K int32, a permutation of [0, K); entries
  * outside [0, K) are clamped) so that groups are contiguous in the stored
- * order and the fast kernels serve the layer.  With M = 1 and a layout the
- * GEMV takes, x is gathered inside the kernel; otherwise the gathered x
- * (gptq_linear_perm_workspace_size bytes) is written to the workspace first.
+ * order and the fast kernels serve the layer.  The gathered x
+ * (gptq_linear_perm_workspace_size bytes) is written to the workspace first,
+ * by one small kernel, then the kernels of gptq_linear read it.
  * Replaces torch.ops.gptq.linear (models/layers.py:151-153) for GPTQ
  * act-order output, whose g_idx (:60) maps input columns to groups out of
  * order; semantics F.linear(x, unpack_weights(), bias) (:155-157). */

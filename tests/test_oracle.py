@@ -354,3 +354,72 @@ def test_bitstream_odd_k_lone_nibble():
     assert p3.shape == (1, 3)
     bits = sum(int(v) << (3 * i) for i, v in enumerate(c3[0]))
     assert int.from_bytes(bytes(p3[0]), "little") == bits
+
+
+# ------------------------------------------------------ sweep replay --
+
+def _replay_case(bits, gs, actorder, seed=0, K=96, N=24):
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((4 * K, K))
+    X[:, :2] *= 8
+    H = X.T @ X
+    W = rng.standard_normal((N, K)) * 0.02
+    r = O.gptq_canonical(W, H, 8, bits, gs, 32, 0.01, actorder=actorder)
+    return W, H, r
+
+
+@pytest.mark.parametrize("bits,gs,actorder", [(4, 32, True), (3, 16, False), (8, -1, True), (2, 24, False)])
+def test_replay_of_own_trajectory_is_exact(bits, gs, actorder):
+    """Replaying the oracle's own codes and parameters gives margin 0 and
+    the same parameters (it is the same loop with the decisions forced)."""
+    W, H, r = _replay_case(bits, gs, actorder)
+    rep = O.gptq_canonical_replay(W, r["U"], r["perm"], np.diag(H) == 0, bits, gs, 32, r["codes"], r["scale"],
+                                  r["zero"])
+    assert rep["margin"].max() == 0.0
+    np.testing.assert_allclose(rep["scale"], r["scale"], rtol=1e-12)
+    np.testing.assert_array_equal(rep["zero"], r["zero"])
+
+
+def test_replay_catches_a_wrong_code_and_a_wrong_update():
+    """A code one step off is outside its cell by (distance to the cell),
+    and a trajectory computed with a dropped update term (the trailing GEMM
+    skipped) is caught at once."""
+    W, H, r = _replay_case(4, 32, False, seed=1)
+    dead = np.diag(H) == 0
+    codes = r["codes"].copy()
+    q = codes[5, 40]
+    codes[5, 40] = q + 1 if q < 15 else q - 1
+    rep = O.gptq_canonical_replay(W, r["U"], r["perm"], dead, 4, 32, 32, codes, r["scale"], r["zero"])
+    assert rep["margin"][5, 40] > 0
+    assert np.all(np.delete(rep["margin"], 5, axis=0) == 0)
+    # decisions of a sweep that skipped the cross-block update (blocksize =
+    # cols without trailing work is the same as eager; here: only
+    # intra-block propagation, as the reference mode does)
+    U = r["U"]
+    Wb = W.copy()
+    Q = np.zeros_like(Wb)
+    s, z = r["scale"], r["zero"]
+    for c in range(W.shape[1]):
+        if c % 32 == 0:
+            blk = Wb[:, c:c + 32].copy()
+        j = c % 32
+        g = c // 32
+        q = np.clip(np.round(blk[:, j] / s[:, g]) + z[:, g], 0, 15)
+        Q[:, c] = q
+        e = (blk[:, j] - s[:, g] * (q - z[:, g])) / U[c, c]
+        blk[:, j:] -= np.outer(e, U[c, c:c - j + 32])
+    rep2 = O.gptq_canonical_replay(W, U, None, dead, 4, 32, 32, Q, s, z)
+    assert rep2["margin"].max() > 0.05
+
+
+def test_replay_zero_tie_detector():
+    """A group whose -xmin / s is exactly k + 1/2 (a symmetric range at 8
+    bits: 255 / 2) is flagged as a tie; an ordinary group is not."""
+    W = np.zeros((2, 4))
+    W[0] = [-0.5, 0.5, 0.25, -0.25]          # xmin = -xmax -> -xmin / s = 127.5
+    W[1] = [-0.3, 0.6, 0.1, 0.2]             # -xmin / s = 85: half a step from a tie
+    U = np.eye(4)
+    r = O.gptq_canonical(W, np.eye(4) * 10, 2, 8, -1, 4, 0.0, U=U)
+    rep = O.gptq_canonical_replay(W, U, None, None, 8, -1, 4, r["codes"], r["scale"], r["zero"])
+    assert rep["zero_margin"][0, 0] == 0.0 and rep["zero_margin"][1, 0] > 0.01
+    assert rep["margin"].max() == 0.0
