@@ -55,6 +55,9 @@ SIGNATURES = {
     "gptq_linear_perm_workspace_size": (_sz, [_i64, _i64, _i]),
     "gptq_linear_perm": (_i, [_p, _i, _i64, _p, _p, _i, _p, _p, _i, _p, _i, _i64, _p, _i, _i64, _i64, _p, _p, _sz,
                               _p]),
+    "gptq_linear_perm_noalloc_max_bytes": (_sz, []),
+    "gptq_linear_perm_noalloc": (_i, [_p, _i, _i64, _p, _p, _i, _p, _p, _i, _p, _i, _i64, _p, _i, _i64, _i64, _p,
+                                      _p]),
     "gptq_quantize_tensor": (_i, [_p, _i, _i64, _i, _i, _i, _p, _p, _p, _p]),
     "gptq_dequantize_tensor": (_i, [_p, _i64, _i, _p, _p, _p, _p]),
 }

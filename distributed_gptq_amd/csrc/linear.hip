@@ -28,6 +28,8 @@
 //    output, fp32.
 #include "common.hpp"
 
+#include <mutex>
+
 namespace gptq {
 namespace {
 
@@ -1687,4 +1689,75 @@ extern "C" int gptq_linear_perm(const void* x, int x_dtype, int64_t M, const int
   if (lrc != GPTQ_OK) return lrc;
   a.x = static_cast<const uint16_t*>(workspace);
   return dispatch_linear(st, a, bits, g_idx);
+}
+
+// ------------------------------------------------- no-allocation variant --
+// gptq_linear_perm_noalloc keeps the gathered activations in `scratch`, a
+// file-scope device array (every GPU the library runs on holds its own copy
+// until the process ends), instead of a caller workspace.  Host code never
+// uses the array's name as an address: at the first call on a device its
+// address on that device is looked up once (hipGetSymbolAddress, with that
+// device current) and kept per device.
+constexpr size_t kNoAllocScratchBytes = size_t(4) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace gptq {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// this device's address of `scratch` (looked up once per device)
+int scratch_address(hipStream_t st, void** out) {
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  GPTQ_REQUIRE(e == hipSuccess, GPTQ_ERR_DEVICE, "linear_perm_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  int dev = cur;
+  if (st != nullptr) {
+    e = hipStreamGetDevice(st, &dev);
+    GPTQ_REQUIRE(e == hipSuccess, GPTQ_ERR_DEVICE, "linear_perm_noalloc: hipStreamGetDevice: %s",
+                 hipGetErrorString(e));
+  }
+  GPTQ_REQUIRE(dev >= 0 && dev < kMaxDevices, GPTQ_ERR_DEVICE, "linear_perm_noalloc: device %d", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    if (dev != cur) {
+      e = hipSetDevice(dev);
+      GPTQ_REQUIRE(e == hipSuccess, GPTQ_ERR_DEVICE, "linear_perm_noalloc: hipSetDevice(%d): %s", dev,
+                   hipGetErrorString(e));
+    }
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    const hipError_t back = dev != cur ? hipSetDevice(cur) : hipSuccess;
+    GPTQ_REQUIRE(e == hipSuccess && p != nullptr, GPTQ_ERR_DEVICE,
+                 "linear_perm_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    GPTQ_REQUIRE(back == hipSuccess, GPTQ_ERR_DEVICE, "linear_perm_noalloc: hipSetDevice(%d): %s", cur,
+                 hipGetErrorString(back));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return GPTQ_OK;
+}
+
+}  // namespace
+}  // namespace gptq
+
+extern "C" size_t gptq_linear_perm_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int gptq_linear_perm_noalloc(const void* x, int x_dtype, int64_t M, const int32_t* perm,
+                                        const uint8_t* packed, int bits, const void* scales, const void* zeros,
+                                        int sz_dtype, const int32_t* g_idx, int group_size, int64_t ngroups,
+                                        const void* bias, int bias_dtype, int64_t N, int64_t K, void* y,
+                                        gptq_stream_t stream) {
+  clear_error();
+  const size_t need = gptq_linear_perm_workspace_size(M, K, x_dtype);
+  GPTQ_REQUIRE(need <= kNoAllocScratchBytes, GPTQ_ERR_WORKSPACE,
+               "linear_perm_noalloc: %lld x %lld activations need %zu bytes of scratch; the limit is %zu",
+               static_cast<long long>(M), static_cast<long long>(K), need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  const int rc = scratch_address(as_hip(stream), &ws);
+  if (rc != GPTQ_OK) return rc;
+  return gptq_linear_perm(x, x_dtype, M, perm, packed, bits, scales, zeros, sz_dtype, g_idx, group_size, ngroups,
+                          bias, bias_dtype, N, K, y, ws, kNoAllocScratchBytes, stream);
 }

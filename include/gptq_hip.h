@@ -228,6 +228,24 @@ int gptq_linear_perm(const void* x, int x_dtype, int64_t M, const int32_t* perm,
                      void* workspace, size_t workspace_bytes,
                      gptq_stream_t stream);
 
+/* gptq_linear_perm without a workspace: for callers that cannot allocate
+ * (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  The gathered activations go
+ * to a static device array of gptq_linear_perm_noalloc_max_bytes() bytes
+ * (4 MiB) that each GPU holds until the process ends; M * K * sizeof(x
+ * element) above that is refused with GPTQ_ERR_WORKSPACE.  Nothing is
+ * allocated or freed.  All calls on one GPU share that array: calls that
+ * overlap on one GPU (different streams, no ordering between them) race.
+ * Otherwise as gptq_linear_perm. */
+size_t gptq_linear_perm_noalloc_max_bytes(void);
+int gptq_linear_perm_noalloc(const void* x, int x_dtype, int64_t M,
+                             const int32_t* perm, const uint8_t* packed,
+                             int bits, const void* scales, const void* zeros,
+                             int sz_dtype, const int32_t* g_idx,
+                             int group_size, int64_t ngroups, const void* bias,
+                             int bias_dtype, int64_t N, int64_t K, void* y,
+                             gptq_stream_t stream);
+
 /* ------------------------------------------------- elementwise quantise --
  * Flat groups of group_size consecutive elements (the tensor API of
  * kernels/triton_kernels.py:377-481): per group s = (max - min) / maxq,
