@@ -398,6 +398,66 @@ def cpu_baseline(seconds_hint=20.0):
                          "sweep_4096x1024": round(t_s, 3)}}
 
 
+# ------------------------------------------------- kernel set for counters --
+
+def run_kernels(args, torch, dev):
+    """The kernels the hardware-counter summaries cover, each launched a few
+    times eagerly (no graphs, so every dispatch is profiled): a device copy
+    of 512 MiB (the FETCH_SIZE / WRITE_SIZE calibration), the down_proj
+    Hessian of the config-3 block (262144 bf16 tokens, K = 14336), the
+    factorisation and 4-bit act-order sweep of a 4096 x 14336 layer, and the
+    W4A16 GEMV / dequant-GEMM at the config-4 shapes for M = 1, 16, 128
+    (8 distinct weight buffers per shape, so that weights come from HBM)."""
+    from distributed_gptq_amd import _ops, pipeline
+    out = {}
+
+    def timed(fn, reps):
+        ts = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        return round(min(ts), 4)
+
+    src = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    out["copy_512MiB_ms"] = timed(lambda: dst.copy_(src), 3)
+    del src, dst
+    g = torch.Generator(device=dev).manual_seed(5)
+    n, K = args.nseq * args.seqlen, FFN
+    X = torch.randn(n, K, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    H = torch.zeros(K, K, device=dev)
+    out["hessian_ms"] = timed(lambda: _ops.hessian_accumulate(H, X), 3)
+    out["hessian_tflops"] = round(hessian_flops(n, K) / (out["hessian_ms"] * 1e-3) / 1e12, 1)
+    del X
+    W = (torch.randn(HID, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    t0 = time.perf_counter()
+    pipeline.quantize_layers({"down_proj": W}, {"down_proj": "down"}, {"down": (H, args.nseq)}, bits=4,
+                             group_size=128, actorder=True, want_dequant=False)
+    torch.cuda.synchronize()
+    out["factor_sweep_s"] = round(time.perf_counter() - t0, 4)
+    del W, H
+    torch.cuda.empty_cache()
+    for (N, Kg) in GEMV_SHAPES:
+        codes = torch.randint(0, 16, (N, Kg), generator=g, device=dev, dtype=torch.uint8)
+        qs = [_ops.pack(codes, 4) for _ in range(8)]
+        sc = (torch.rand(N, Kg // 128, generator=g, device=dev) * 9e-3 + 1e-3).half()
+        zr = torch.full((N, Kg // 128), 8.0, device=dev, dtype=torch.float16)
+        for M in (1, 16, 128):
+            x = torch.randn(M, Kg, generator=g, device=dev).half()
+
+            def run(x=x):
+                for q in qs:
+                    _ops.linear(x, q, 4, sc, zr, Kg, group_size=128)
+            out[f"w4a16_{N}x{Kg}_m{M}_us"] = round(timed(run, 2) * 1e3 / len(qs), 2)
+        del qs, codes
+        torch.cuda.empty_cache()
+    return out
+
+
 # ------------------------------------------------ whole-model workloads --
 # Config 2 (OPT-125m shape) and config 5 (13B shape): random-init models built
 # from transformers' architectures, calibrated on uniform random token ids and
@@ -462,7 +522,8 @@ def run_model(args, torch, dev):
     for idx, (bits, gs, actorder) in enumerate(settings):
         timed = idx >= args.warmup
         model = copy.deepcopy(base)
-        cfg = QuantizationConfig(bits=bits, group_size=gs, actorder=actorder, calibration_samples=nseq)
+        cfg = QuantizationConfig(bits=bits, group_size=gs, actorder=actorder, calibration_samples=nseq,
+                                 true_sequential=args.true_sequential)
         dq = DistributedGPTQuantizer(cfg)
         torch.cuda.synchronize()
         torch.cuda.reset_peak_memory_stats()
@@ -477,7 +538,8 @@ def run_model(args, torch, dev):
         wall = time.perf_counter() - t0
         free1, _ = torch.cuda.mem_get_info()
         errs = dq.quantization_errors
-        r = {"bits": bits, "group_size": gs, "actorder": actorder, "wall_s": round(wall, 3),
+        r = {"bits": bits, "group_size": gs, "actorder": actorder, "true_sequential": args.true_sequential,
+             "wall_s": round(wall, 3),
              "layers": len(errs), "peak_allocated_GiB": round(torch.cuda.max_memory_allocated() / 2**30, 2),
              "device_used_GiB_after": round((total - free1) / 2**30, 2),
              "total_error": float(sum(errs.values()))}
@@ -505,9 +567,11 @@ def main():
     ap.add_argument("--no-gemv", action="store_true")
     ap.add_argument("--no-block", action="store_true")
     ap.add_argument("--no-3bit", action="store_true", help="skip the 3-bit block run")
-    ap.add_argument("--workload", choices=["block", *MODELS], default="block",
+    ap.add_argument("--workload", choices=["block", "kernels", *MODELS], default="block",
                     help="block: config 3 (default); opt125m: config 2; llama13b: config 5")
     ap.add_argument("--model-nseq", type=int, default=0, help="calibration sequences for a model workload")
+    ap.add_argument("--true-sequential", action="store_true",
+                    help="model workloads: quantize block by block (QuantizationConfig.true_sequential)")
     ap.add_argument("--model-chunk", type=int, default=0, help="sequences per calibration forward (model workloads)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -521,6 +585,10 @@ def main():
     import distributed_gptq_amd  # noqa: F401
     from distributed_gptq_amd import _lib
     _lib.load()
+    if args.workload == "kernels":
+        print(json.dumps({"workload": "kernels (the set the counter summaries cover)",
+                          **run_kernels(args, torch, dev)}), flush=True)
+        return
     if args.workload != "block":
         m = run_model(args, torch, dev)
         spec = MODELS[args.workload]
