@@ -22,6 +22,8 @@
 //    v_mfma_f32_16x16x32_{f16,bf16} (dq_split_k: the waves of a workgroup
 //    split K over 128-column blocks and reduce through LDS; dq_tile_k:
 //    128-row weight tiles x 64/128 activation rows, double-buffered LDS).
+//  * dq_rx_k (64 < M <= 128, wide layers): the codes are decoded in registers
+//    straight into the MFMA operands; X is staged in LDS by loader waves.
 //  * dq_mfma_k (other M > 4 layouts): 16 weight rows x 16 activation rows per
 //    MFMA step with zero points folded per group, 4 waves splitting K.
 //  * linear_generic: any layout (fp32 x, g_idx, ragged K): one wave per
@@ -1402,6 +1404,246 @@ __global__ __launch_bounds__(256) void dq_tile_k(LinArgs a) {
       }
 }
 
+// Large products with 4- or 3-bit codes (M > 64, K % 128 == 0, group size %
+// 32 == 0, wide layers): the weights never pass through LDS.  A workgroup
+// owns NW * WAVES weight rows x MT activation rows over the whole of K, with
+// WAVES compute waves and L loader waves.  Per 128-column block the loaders
+// stage the workgroup's MT x 128 piece of X in LDS (double-buffered, each
+// 8-column piece permuted into the order the codes decode in) and every
+// compute wave reads all of it.  A compute wave's NW rows are its own: lane
+// (r, g) loads codes 32 g .. 32 g + 31 of row r (the column bijection of
+// dq_reg4_k), decodes the block's four words into the A operands of its four
+// MFMA steps ((q - z) exact, one rounding of the product by s, as in the LDS
+// paths) and multiplies each against the MT / 16 X fragments of its step, so
+// a code is decoded once and used MT times.  Loads complete in issue order per
+// wave, so the X loads live in their own waves: a compute wave's queue holds
+// only codes and scales, kept S blocks ahead in S register slots.
+template <int NW, int BITS>
+struct RxCodes {
+  uint32_t cw[NW / 16][BITS];
+  uint32_t sw[NW / 16], zw[NW / 16];
+  bool sh[NW / 16], zh[NW / 16];
+};
+
+template <int BITS, bool BF16, int NW, int WAVES, int L, int MT, int S, int OCC>
+__global__ __launch_bounds__(64 * (WAVES + L)) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void dq_rx_k(LinArgs a) {
+  static_assert(BITS == 4 || BITS == 3, "4- or 3-bit codes");
+  constexpr int NB = NW / 16, MB = MT / 16;
+  constexpr int P = 128 + 8;              // LDS row pitch (halves)
+  constexpr int XP = MT * 16 / (64 * L);  // 16-byte X pieces per loader lane and block
+  static_assert(NW % 16 == 0 && MT % 16 == 0 && (MT * 16) % (64 * L) == 0 && S >= 2, "tile shape");
+  __shared__ __attribute__((aligned(16))) uint16_t sX[2][MT * P];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * MT;
+  const int nblk = static_cast<int>(a.K / 128);
+  const int nsteps = static_cast<int>(cdiv(nblk, S)) * S;  // whole rounds of the S code slots
+
+  if (wave >= WAVES) {
+    // loaders: piece e = 64 (wave - WAVES) + 64 L v + lane is row e / 16,
+    // columns 8 (e % 16) .. + 7 of the block, read through a buffer descriptor
+    // that ends at the last row of X (rows past M read as zeros, with no
+    // address arithmetic per piece)
+    const int e0 = 64 * (wave - WAVES) + lane;
+    const int64_t rows = std::min<int64_t>(MT, a.M - m0);
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x + m0 * a.K, static_cast<uint32_t>(rows * a.K * 2));
+    const uint32_t voff = static_cast<uint32_t>((e0 / 16) * a.K * 2 + 16 * (e0 % 16));
+    uint4 xr[XP];
+    auto load_x = [&](int b) {
+#pragma unroll
+      for (int v = 0; v < XP; ++v) {
+        const uint32_t off = static_cast<uint32_t>((4 * L * v * a.K + static_cast<int64_t>(b) * 128) * 2);
+        xr[v] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, voff + off, 0, 0));
+      }
+    };
+    auto store_x = [&](int buf) {
+#pragma unroll
+      for (int v = 0; v < XP; ++v) {
+        const int e = e0 + 64 * L * v;
+        *reinterpret_cast<uint4*>(&sX[buf][(e / 16) * P + 8 * (e % 16)]) = perm_0415(xr[v]);
+      }
+    };
+    load_x(0);
+    store_x(0);
+    if (nblk > 1) load_x(1);
+    __syncthreads();
+    for (int j = 0; j < nsteps; ++j) {
+      if (j + 1 < nblk) {
+        store_x((j + 1) & 1);
+        if (j + 2 < nblk) load_x(j + 2);
+      }
+      __syncthreads();
+    }
+    return;
+  }
+
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * (NW * WAVES) + NW * wave;
+  const uint8_t* wrow[NB];
+  int64_t wn[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    wn[i] = std::min<int64_t>(n0 + 16 * i + r16, a.N - 1);
+    wrow[i] = a.packed + wn[i] * a.pitch;
+  }
+  using Cd = RxCodes<NW, BITS>;
+  auto load_codes = [&](int b, Cd& C) {
+    const int64_t k = static_cast<int64_t>(b) * 128 + 32 * g4;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(wrow[i] + k * BITS / 8);
+      if constexpr (BITS == 4) {
+        const uint4 v = *reinterpret_cast<const uint4*>(src);
+        C.cw[i][0] = v.x; C.cw[i][1] = v.y; C.cw[i][2] = v.z; C.cw[i][3] = v.w;
+      } else {
+        C.cw[i][0] = src[0]; C.cw[i][1] = src[1]; C.cw[i][2] = src[2];
+      }
+    }
+    const int64_t g = static_cast<int>(k) / a.gs;  // 32-bit division (K < 2^31)
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      C.sw[i] = elem_word(a.scales, wn[i] * a.ngroups + g, a.sz_dtype, C.sh[i]);
+      C.zw[i] = elem_word(a.zeros, wn[i] * a.ngroups + g, a.sz_dtype, C.zh[i]);
+    }
+  };
+
+  auto mfma = [](uint4 fa, uint4 fb, f32x4 c) {
+    if constexpr (BF16)
+      return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, fa), __builtin_bit_cast(bf16x8, fb), c,
+                                                     0, 0, 0);
+    else
+      return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, fa), __builtin_bit_cast(f16x8, fb), c, 0,
+                                                    0, 0);
+  };
+  // GPTQ zero points are integers: with fp16 activations and every zero of
+  // the wave's rows an integer in [0, 1023] the decode is packed fp16 math
+  // ((1024 + q) - (1024 + z) exact, then * s), decided once
+  bool pk = !BF16;
+  if constexpr (!BF16) {
+    for (int64_t g = g4; g < a.ngroups; g += 4)
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const float z = load_elem(a.zeros, wn[i] * a.ngroups + g, a.sz_dtype);
+        pk = pk && z == rintf(z) && z >= 0.0f && z <= 1023.0f;
+      }
+    pk = __all(pk);
+  }
+
+  f32x4 acc[NB][MB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int j = 0; j < MB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // a block: its weight fragments are decoded first (one wave-uniform
+  // branch between the packed and the fp32 decode), then the four MFMA steps
+  // run as a software pipeline, the X fragments of step kk + 1 read while
+  // step kk is multiplied (the scheduling groups fix that order; left alone
+  // the compiler waits for each fragment right before its MFMA)
+  auto compute = [&](int buf, const Cd& C) {
+    uint4 fa[4][NB];
+    auto decode = [&](auto packed) {
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const float s = elem_value(C.sw[i], C.sh[i], a.sz_dtype);
+        const float z = elem_value(C.zw[i], C.zh[i], a.sz_dtype);
+        const uint32_t zz = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(1024.0f + z),
+                                                                static_cast<_Float16>(1024.0f + z)});
+        const uint32_t sh = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(s), static_cast<_Float16>(s)});
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          uint32_t pr[4];
+          step_pairs<BITS>(C.cw[i], kk, pr);
+          if constexpr (decltype(packed)::value)
+            fa[kk][i] = dq_word_0415<true>(pr, zz, sh, 0.0f, 0.0f);
+          else
+            fa[kk][i] = dq_word_0415<false, BF16>(pr, 0u, 0u, s, z);
+        }
+      }
+    };
+    if (pk)
+      decode(std::true_type{});
+    else
+      decode(std::false_type{});
+    const uint16_t* xs = &sX[buf][r16 * P + 32 * g4];
+    uint4 fb[2][MB];
+#pragma unroll
+    for (int j = 0; j < MB; ++j) fb[0][j] = *reinterpret_cast<const uint4*>(xs + 16 * j * P);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int c = kk & 1, n = c ^ 1;
+      if (kk + 1 < 4) {
+#pragma unroll
+        for (int j = 0; j < MB; ++j) fb[n][j] = *reinterpret_cast<const uint4*>(xs + 16 * j * P + 8 * (kk + 1));
+      }
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+#pragma unroll
+        for (int j = 0; j < MB; ++j) acc[i][j] = mfma(fa[kk][i], fb[c][j], acc[i][j]);
+      if (kk + 1 < 4) {
+        __builtin_amdgcn_sched_group_barrier(0x100, MB, 0);       // the next step's X fragments first
+        __builtin_amdgcn_sched_group_barrier(0x008, NB * MB, 0);  // then this step's MFMAs
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // block j is multiplied from slot j % S, which then takes the codes of
+  // block j + S.  The loads are unconditional (past the last block they
+  // repeat it) and the steps come in whole rounds, so every path through the
+  // loop issues the same loads and each wait is for the oldest slot only.
+  Cd C[S];
+#pragma unroll
+  for (int u = 0; u < S; ++u) load_codes(std::min(u, nblk - 1), C[u]);
+  __syncthreads();
+  for (int j0 = 0; j0 < nsteps; j0 += S) {
+#pragma unroll
+    for (int u = 0; u < S; ++u) {
+      const int j = j0 + u;
+      if (j < nblk) compute(j & 1, C[u]);
+      load_codes(std::min(j + S, nblk - 1), C[u]);
+      __syncthreads();
+    }
+  }
+
+  // 16x16 layout: lane l, register v -> weight row 4 (l / 16) + v, X row l % 16;
+  // four consecutive outputs of a row go out as one 8-byte store
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int64_t n = n0 + 16 * i + 4 * g4;
+    float bv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (a.bias) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (n + v < a.N) bv[v] = load_elem(a.bias, n + v, a.bias_dtype);
+    }
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const int64_t m = m0 + 16 * j + r16;
+      if (m >= a.M) continue;
+      const float r[4] = {acc[i][j][0] + bv[0], acc[i][j][1] + bv[1], acc[i][j][2] + bv[2], acc[i][j][3] + bv[3]};
+      if (a.y_dtype != GPTQ_F32 && n + 3 < a.N && (a.N & 3) == 0) {
+        uint32_t h[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) h[v] = a.y_dtype == GPTQ_BF16 ? f32_to_bf16_bits(r[v]) : f32_to_f16_bits(r[v]);
+        *reinterpret_cast<uint2*>(a.y + m * a.N + n) = uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (n + v < a.N) store_elem(a.y, m * a.N + n + v, a.y_dtype, r[v]);
+      }
+    }
+  }
+}
+
+template <int BITS, bool BF16, int NW, int WAVES, int L, int MT, int S, int OCC>
+int launch_rx(hipStream_t st, const LinArgs& a) {
+  const dim3 grid(static_cast<unsigned>(cdiv(a.N, NW * WAVES)), static_cast<unsigned>(cdiv(a.M, MT)));
+  hipLaunchKernelGGL((dq_rx_k<BITS, BF16, NW, WAVES, L, MT, S, OCC>), grid, dim3(64 * (WAVES + L)), 0, st, a);
+  return check_launch("dq_rx");
+}
+
 template <int BITS, bool BF16, int NT, int MT, int WAVES>
 int launch_split(hipStream_t st, const LinArgs& a) {
   using C = DsCfg<NT, MT, WAVES>;
@@ -1431,6 +1673,14 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
       if (a.N >= 32 * 256) return launch_reg4<BITS, 64, 8, BF16>(st, a);
       return launch_reg4<BITS, 16, 8, BF16>(st, a);
     }
+  }
+  if constexpr (BITS == 4 || BITS == 3) {
+    // 64 < M <= 128 on wide layers (>= 192 workgroups of 128 rows): the
+    // register-decoded kernel, one workgroup per CU (measured on MI355X at
+    // 28672 x 4096, M = 128: 69 against 98 us (4-bit), 71 against 116 us
+    // (3-bit); at M = 64 and on narrower layers the tile kernels are faster)
+    if (a.M > 64 && a.M <= 128 && a.N >= 192 * 128 && (BITS == 4 || a.pitch % 4 == 0))
+      return launch_rx<BITS, BF16, 16, 8, 2, 128, 4, 2>(st, a);
   }
   if (a.M <= 16) {
     if (a.N >= 64 * 256) return launch_split<BITS, BF16, 64, 16, 8>(st, a);

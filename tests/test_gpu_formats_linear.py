@@ -251,6 +251,35 @@ def test_linear_dequant_gemm(hip, xdt, bits, M, N, K, gs):
 
 
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bits", [3, 4])
+@pytest.mark.parametrize("M,N,K,gs,zkind,sdt", [
+    (128, 24576, 512, 128, "int", torch.float16),
+    # ragged last workgroup (N % 128 = 4) and block count below the code slots
+    (100, 24580, 384, 64, "int", torch.float16),
+    # N % 4 != 0 (element stores), groups of 32 (a lane's chunk in its own group)
+    (65, 24578, 256, 32, "int", torch.float16),
+    # zeros that are not integers (the fp32 decode for fp16 activations) and fp32 scales
+    (128, 24576, 640, 128, "frac", torch.float16),
+    (128, 24576, 1152, 128, "int", torch.float32)])
+def test_linear_register_decoded_wide(hip, xdt, bits, M, N, K, gs, zkind, sdt):
+    """64 < M <= 128 on layers of >= 192 x 128 rows: the kernel that decodes
+    the codes in registers (loader waves stage X), against the fp64 oracle."""
+    from distributed_gptq_amd import _ops
+    codes, scales, zeros, x = _case(M, N, K, bits, gs, M + N + bits + K, xdt)
+    if zkind == "frac":
+        rng = np.random.default_rng(N + K)
+        zeros = torch.from_numpy(rng.uniform(0, 2 ** bits - 1, zeros.shape)).half()
+    scales, zeros = scales.to(sdt), zeros.to(sdt)
+    bias = torch.randn(N).to(xdt)
+    packed = torch.from_numpy(O.pack_bitstream(codes, bits)).cuda()
+    y = _ops.linear(x.cuda(), packed, bits, scales.cuda(), zeros.cuda(), K, group_size=gs, bias=bias.cuda())
+    ref = O.linear(x.float().numpy(), codes, scales.float().numpy(), zeros.float().numpy(), np.arange(K) // gs,
+                   bias.float().numpy())
+    err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err < TOL[xdt], err
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("M,N", [(1, 1030), (3, 1030), (16, 4101), (128, 8256)])
 def test_linear_scales_at_odd_offset(hip, xdt, M, N):
     """Scales and zeros whose base is 2 but not 4-byte aligned (a contiguous
