@@ -518,7 +518,10 @@ def run_model(args, torch, dev):
     data = [ids[i:i + chunk] for i in range(0, nseq, chunk)]
     runs = []
     # untimed warm-up runs of the first setting (library initialisation, GEMM heuristics)
-    settings = [spec["runs"][0]] * args.warmup + list(spec["runs"])
+    chosen = [r for r in spec["runs"] if not args.model_bits or r[0] in args.model_bits]
+    if not chosen:
+        raise SystemExit(f"--model-bits {args.model_bits}: no run of {args.workload} has those bits")
+    settings = [chosen[0]] * args.warmup + chosen
     for idx, (bits, gs, actorder) in enumerate(settings):
         timed = idx >= args.warmup
         model = copy.deepcopy(base)
@@ -570,6 +573,8 @@ def main():
     ap.add_argument("--workload", choices=["block", "kernels", *MODELS], default="block",
                     help="block: config 3 (default); opt125m: config 2; llama13b: config 5")
     ap.add_argument("--model-nseq", type=int, default=0, help="calibration sequences for a model workload")
+    ap.add_argument("--model-bits", type=lambda v: [int(b) for b in v.split(",")], default=None,
+                    help="only the runs of a model workload with these code widths (comma list)")
     ap.add_argument("--true-sequential", action="store_true",
                     help="model workloads: quantize block by block (QuantizationConfig.true_sequential)")
     ap.add_argument("--model-chunk", type=int, default=0, help="sequences per calibration forward (model workloads)")

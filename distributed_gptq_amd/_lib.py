@@ -51,6 +51,7 @@ SIGNATURES = {
     "gptq_unpack": (_i, [_p, _i64, _i64, _i, _p, _p]),
     "gptq_pack_reference_layout": (_i, [_p, _i64, _i64, _i, _p, _p]),
     "gptq_dequant": (_i, [_p, _i, _p, _p, _i, _p, _i, _i64, _i64, _i64, _p, _p]),
+    "gptq_dequant_to": (_i, [_p, _i, _p, _p, _i, _p, _i, _i64, _i64, _i64, _p, _i, _p]),
     "gptq_linear": (_i, [_p, _i, _i64, _p, _i, _p, _p, _i, _p, _i, _i64, _p, _i, _i64, _i64, _p, _p]),
     "gptq_linear_perm_workspace_size": (_sz, [_i64, _i64, _i]),
     "gptq_linear_perm": (_i, [_p, _i, _i64, _p, _p, _i, _p, _p, _i, _p, _i, _i64, _p, _i, _i64, _i64, _p, _p, _sz,

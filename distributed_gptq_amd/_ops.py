@@ -226,8 +226,10 @@ def pack_reference_layout(codes: torch.Tensor, bits: int) -> torch.Tensor:
 
 
 def dequant(packed: torch.Tensor, bits: int, scales: torch.Tensor, zeros: torch.Tensor, K: int,
-            g_idx: torch.Tensor | None = None, group_size: int = 0) -> torch.Tensor:
-    """bits == 0: one code per byte (N x K)."""
+            g_idx: torch.Tensor | None = None, group_size: int = 0,
+            dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """(N x K) weights in ``dtype`` (fp32, or rounded once to fp16 / bf16).
+    bits == 0: one code per byte (N x K)."""
     _gpu(packed, scales, zeros)
     packed = packed.contiguous()
     scales = scales.contiguous()
@@ -236,9 +238,9 @@ def dequant(packed: torch.Tensor, bits: int, scales: torch.Tensor, zeros: torch.
     ng = scales.shape[1]
     if g_idx is not None:
         g_idx = g_idx.to(device=packed.device, dtype=torch.int32).contiguous()
-    out = torch.empty((N, K), dtype=torch.float32, device=packed.device)
-    L.call("gptq_dequant", _p(packed), bits, _p(scales), _p(zeros), dtype_code(scales.dtype), _p(g_idx), group_size,
-           ng, N, K, _p(out), _stream(packed.device))
+    out = torch.empty((N, K), dtype=dtype, device=packed.device)
+    L.call("gptq_dequant_to", _p(packed), bits, _p(scales), _p(zeros), dtype_code(scales.dtype), _p(g_idx),
+           group_size, ng, N, K, _p(out), dtype_code(dtype), _stream(packed.device))
     return out
 
 

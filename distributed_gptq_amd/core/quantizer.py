@@ -204,7 +204,8 @@ class _HookError(RuntimeError):
 
 
 class _StopForward(Exception):
-    """Ends a calibration forward once the first block's inputs are taken."""
+    """Ends a calibration forward early: once the first block's inputs are
+    taken, or once the last layer a pass calibrates has run."""
 
 
 def _find_blocks(model: nn.Module, layers: Dict[str, nn.Linear]):
@@ -456,11 +457,12 @@ class DistributedGPTQuantizer:
 
     @torch.no_grad()
     def _collect_hessians(self, model: nn.Module, calibration_data, layers: Dict[str, nn.Linear],
-                          batches=None) -> _SharedHessians:
+                          batches=None, stop_after: bool = False) -> _SharedHessians:
         """Calibration forward (:194-246) with the Hessians accumulated in the
         hooks.  ``batches`` (an iterator that runs one forward per step and
         yields whether it ran) defaults to the whole model over
-        ``calibration_data``."""
+        ``calibration_data``; with ``stop_after`` each forward ends (by
+        _StopForward, which ``batches`` catches) once every layer has run."""
         hs = _SharedHessians(layers, self.device, self.share_hessians)
         self._call_order: List[str] = []
 
@@ -476,6 +478,8 @@ class DistributedGPTQuantizer:
             return hook
 
         handles = [m.register_forward_hook(hook_for(n)) for n, m in layers.items()]
+        if stop_after:
+            handles += self._stop_hooks(layers)
         it = batches if batches is not None else self._model_batches(model, calibration_data)
         ok = 0
         try:
@@ -593,20 +597,39 @@ class DistributedGPTQuantizer:
         if not inputs:
             raise ValueError("no calibration batch reached the first block")
         cfg_model = getattr(model, "config", None)
+        # true sequential: the layer groups of a block in forward order, as
+        # name suffixes, learnt from the first full pass over a block
+        plan: Optional[List[List[str]]] = None
         for i, block in enumerate(mods):
-            mine = {n: m for n, m in layers.items() if n.startswith(f"{prefix}.{i}.")}
+            pre = f"{prefix}.{i}."
+            mine = {n: m for n, m in layers.items() if n.startswith(pre)}
+            step = 0
             while mine:
+                # a planned group is calibrated alone: hooks on its layers only,
+                # and the block's forward stops after the last of them has run
+                want = None
+                if true_sequential and plan is not None and step < len(plan):
+                    names = [pre + sfx for sfx in plan[step]]
+                    if all(n in mine for n in names):
+                        want = {n: mine[n] for n in names}
+
                 def batches(block=block):
                     for args, kwargs in inputs:
-                        block(*args, **kwargs)
+                        try:
+                            block(*args, **kwargs)
+                        except _StopForward:
+                            pass
                         yield True
-                hs = self._collect_hessians(model, None, mine, batches=batches())
+                hs = self._collect_hessians(model, None, want if want is not None else mine, batches=batches(),
+                                            stop_after=want is not None)
                 groups = hs.groups()
                 if true_sequential:
                     # the group of the first layer the forward reached; the
                     # other Hessians saw unquantized predecessors: dropped
                     first = next(n for n in self._call_order if n in mine)
                     gids = [next(g for g, m in groups.items() if first in m)]
+                    if want is None and step == 0 and plan is None:
+                        plan = self._group_plan(groups, pre)
                 else:
                     gids = list(groups)
                 self._quantize_groups(model, hs, gids, mine, progress, counter)
@@ -614,6 +637,7 @@ class DistributedGPTQuantizer:
                 for g in groups:
                     hs.acc[g].free()
                 mine = {n: m for n, m in mine.items() if n not in done}
+                step += 1
             # this block's outputs (its layers now quantized) feed the next
             for j, (args, kwargs) in enumerate(inputs):
                 out = block(*args, **kwargs)
@@ -626,6 +650,32 @@ class DistributedGPTQuantizer:
             hs = self._collect_hessians(model, calibration_data, rest)
             self._quantize_groups(model, hs, list(hs.groups()), rest, progress, counter)
         del cfg_model
+
+    def _group_plan(self, groups, pre: str) -> Optional[List[List[str]]]:
+        """The Hessian groups of a block's first pass in the order the forward
+        reached them, as name suffixes (None if a layer ran twice or a group
+        was never reached)."""
+        order = {n: k for k, n in enumerate(self._call_order)}
+        if any(n not in order for m in groups.values() for n in m):
+            return None
+        ranked = sorted(groups.values(), key=lambda m: min(order[n] for n in m))
+        return [[n[len(pre):] for n in sorted(m, key=lambda n: order[n])] for m in ranked]
+
+    @staticmethod
+    def _stop_hooks(layers: Dict[str, nn.Linear]) -> list:
+        """Forward hooks that end a forward once every layer of ``layers`` has
+        run in it (registered after the Hessian hooks, so they run after the
+        last of them)."""
+        left, seen = set(layers), set()
+
+        def make(name):
+            def hook(module, inp, out):
+                seen.add(name)
+                if seen >= left:
+                    seen.clear()
+                    raise _StopForward
+            return hook
+        return [m.register_forward_hook(make(n)) for n, m in layers.items()]
 
     def _capture_block_inputs(self, model, calibration_data, first_block) -> List[Tuple[tuple, dict]]:
         """(args, kwargs) of the first block's call in each calibration

@@ -777,27 +777,6 @@ struct DsCfg {
   static constexpr size_t kLds = WAVES * kTile + static_cast<size_t>(NT) * MT * 4;
 };
 
-// the 32 codes of a chunk as 16 pairs (codes 2p, 2p + 1 in the low / high halves)
-template <int BITS, int PP>
-__device__ __forceinline__ uint32_t chunk_pair(const uint32_t (&w)[BITS]) {
-  if constexpr (BITS == 4) {
-    const uint32_t v = (w[PP / 4] >> (8 * (PP % 4))) & 0xFFu;
-    return (v & 0xFu) | ((v >> 4) << 16);
-  } else if constexpr (BITS == 2) {
-    const uint32_t v = (w[PP / 8] >> (4 * (PP % 8))) & 0xFu;
-    return (v & 0x3u) | ((v >> 2) << 16);
-  } else if constexpr (BITS == 8) {
-    const uint32_t v = w[PP / 2] >> (16 * (PP % 2));
-    return (v & 0xFFu) | ((v & 0xFF00u) << 8);
-  } else {
-    constexpr int b0 = 6 * PP, d = b0 / 32, o = b0 % 32;
-    uint64_t v = w[d];
-    if constexpr (d + 1 < 3) v |= static_cast<uint64_t>(w[d + 1]) << 32;
-    v >>= o;
-    return static_cast<uint32_t>(v & 7u) | (static_cast<uint32_t>((v >> 3) & 7u) << 16);
-  }
-}
-
 // dequantised pair (exact (q - z), one rounding of the product by s), fp32 arithmetic
 template <bool BF16>
 __device__ __forceinline__ uint32_t dq_pair(uint32_t c, float s, float z) {

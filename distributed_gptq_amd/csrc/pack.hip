@@ -6,6 +6,8 @@
 // bytes; unpacking reads the one or two bytes that hold a code.
 #include "common.hpp"
 
+#include <utility>
+
 namespace gptq {
 namespace {
 
@@ -97,9 +99,11 @@ __global__ void pack_ref_layout_k(const uint8_t* __restrict__ codes, int64_t N, 
 }
 
 #pragma clang fp contract(off)
+// (q - z) * s in fp32 (no FMA), stored as fp32 or rounded to fp16 / bf16
 __global__ void dequant_k(const uint8_t* __restrict__ packed, int bits, const void* __restrict__ scales,
                           const void* __restrict__ zeros, int sz_dtype, const int32_t* __restrict__ g_idx, int gs,
-                          int64_t ngroups, int64_t N, int64_t K, float* __restrict__ out, int64_t pitch) {
+                          int64_t ngroups, int64_t N, int64_t K, void* __restrict__ out, int out_dtype,
+                          int64_t pitch) {
   const int64_t total = N * K;
   for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
        idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
@@ -110,7 +114,74 @@ __global__ void dequant_k(const uint8_t* __restrict__ packed, int bits, const vo
     const float z = load_elem(zeros, n * ngroups + g, sz_dtype);
     const float s = load_elem(scales, n * ngroups + g, sz_dtype);
     const float d = q - z;
-    out[idx] = d * s;
+    store_elem(out, idx, out_dtype, d * s);
+  }
+}
+
+template <int BITS, int PP>
+__device__ __forceinline__ void dequant_pair(const uint32_t (&w)[BITS], float z, float s, float (&v)[32]) {
+  const uint32_t cp = chunk_pair<BITS, PP>(w);
+  const float d0 = static_cast<float>(cp & 0xFFFFu) - z, d1 = static_cast<float>(cp >> 16) - z;
+  v[2 * PP] = d0 * s;
+  v[2 * PP + 1] = d1 * s;
+}
+template <int BITS, int... PP>
+__device__ __forceinline__ void dequant_pairs(const uint32_t (&w)[BITS], float z, float s, float (&v)[32],
+                                              std::integer_sequence<int, PP...>) {
+  (dequant_pair<BITS, PP>(w, z, s, v), ...);
+}
+
+// The same for K % 32 == 0 and groups of a multiple of 32 columns: one thread
+// per 32-code chunk (one group), one 4 * BITS-byte load and 64 (128 for fp32)
+// contiguous bytes stored; consecutive threads take consecutive chunks.
+template <int BITS>
+__global__ __launch_bounds__(256) void dequant_chunks_k(const uint8_t* __restrict__ packed,
+                                                        const void* __restrict__ scales,
+                                                        const void* __restrict__ zeros, int sz_dtype, int gs,
+                                                        int64_t ngroups, int64_t N, int64_t nch, int64_t pitch,
+                                                        void* __restrict__ out, int out_dtype) {
+  const int64_t total = N * nch;
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t n = idx / nch, c = idx - n * nch;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(packed + n * pitch + c * 4 * BITS);
+    uint32_t w[BITS];
+    if constexpr (BITS == 4) {
+      const uint4 v = *reinterpret_cast<const uint4*>(src);
+      w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else if constexpr (BITS == 8) {
+      const uint4 v0 = reinterpret_cast<const uint4*>(src)[0], v1 = reinterpret_cast<const uint4*>(src)[1];
+      w[0] = v0.x; w[1] = v0.y; w[2] = v0.z; w[3] = v0.w; w[4] = v1.x; w[5] = v1.y; w[6] = v1.z; w[7] = v1.w;
+    } else if constexpr (BITS == 2) {
+      const uint2 v = *reinterpret_cast<const uint2*>(src);
+      w[0] = v.x; w[1] = v.y;
+    } else {
+      w[0] = src[0]; w[1] = src[1]; w[2] = src[2];
+    }
+    const int64_t g = (c * 32) / gs;
+    const float z = load_elem(zeros, n * ngroups + g, sz_dtype);
+    const float s = load_elem(scales, n * ngroups + g, sz_dtype);
+    float v[32];
+    dequant_pairs<BITS>(w, z, s, v, std::make_integer_sequence<int, 16>{});
+    if (out_dtype == GPTQ_F32) {
+      uint4* dst = reinterpret_cast<uint4*>(static_cast<float*>(out) + idx * 32);
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        dst[q] = uint4{__float_as_uint(v[4 * q]), __float_as_uint(v[4 * q + 1]), __float_as_uint(v[4 * q + 2]),
+                       __float_as_uint(v[4 * q + 3])};
+    } else {
+      const bool bf = out_dtype == GPTQ_BF16;
+      uint32_t h[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const uint32_t lo = bf ? f32_to_bf16_bits(v[2 * q]) : f32_to_f16_bits(v[2 * q]);
+        const uint32_t hi = bf ? f32_to_bf16_bits(v[2 * q + 1]) : f32_to_f16_bits(v[2 * q + 1]);
+        h[q] = lo | (hi << 16);
+      }
+      uint4* dst = reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + idx * 32);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) dst[q] = uint4{h[4 * q], h[4 * q + 1], h[4 * q + 2], h[4 * q + 3]};
+    }
   }
 }
 
@@ -215,20 +286,44 @@ extern "C" int gptq_pack_reference_layout(const uint8_t* codes, int64_t N, int64
   return check_launch("pack_reference_layout");
 }
 
-extern "C" int gptq_dequant(const uint8_t* packed, int bits, const void* scales, const void* zeros, int sz_dtype,
-                            const int32_t* g_idx, int group_size, int64_t ngroups, int64_t N, int64_t K, float* out,
-                            gptq_stream_t stream) {
+extern "C" int gptq_dequant_to(const uint8_t* packed, int bits, const void* scales, const void* zeros, int sz_dtype,
+                               const int32_t* g_idx, int group_size, int64_t ngroups, int64_t N, int64_t K, void* out,
+                               int out_dtype, gptq_stream_t stream) {
   clear_error();
   GPTQ_REQUIRE(packed && scales && zeros && out, GPTQ_ERR_ARG, "dequant: null pointer");
   GPTQ_REQUIRE(bits == 0 || valid_bits(bits), GPTQ_ERR_ARG, "dequant: bits=%d", bits);
-  GPTQ_REQUIRE(valid_dtype(sz_dtype), GPTQ_ERR_DTYPE, "dequant: bad scale dtype");
+  GPTQ_REQUIRE(valid_dtype(sz_dtype) && valid_dtype(out_dtype), GPTQ_ERR_DTYPE, "dequant: bad scale or output dtype");
   GPTQ_REQUIRE(N > 0 && K > 0 && ngroups > 0 && (g_idx || group_size > 0), GPTQ_ERR_SHAPE, "dequant: bad shape");
   GPTQ_REQUIRE(g_idx || cdiv(K, group_size) <= ngroups, GPTQ_ERR_SHAPE, "dequant: %lld groups < ceil(K/g)",
                (long long)ngroups);
   const int64_t pitch = bits == 0 ? K : pitch_of(K, bits);
-  hipLaunchKernelGGL(dequant_k, dim3(blocks_for(N * K)), dim3(256), 0, as_hip(stream), packed, bits, scales, zeros,
-                     sz_dtype, g_idx, group_size, ngroups, N, K, out, pitch);
+  hipStream_t st = as_hip(stream);
+  const bool aligned = (reinterpret_cast<uintptr_t>(packed) % 16) == 0 && (reinterpret_cast<uintptr_t>(out) % 16) == 0;
+  if (!g_idx && bits != 0 && K % 32 == 0 && group_size % 32 == 0 && aligned) {
+    const int64_t nch = K / 32;
+    const unsigned blocks = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(cdiv(N * nch, 256), 16384)));
+    switch (bits) {
+      case 4: hipLaunchKernelGGL(dequant_chunks_k<4>, dim3(blocks), dim3(256), 0, st, packed, scales, zeros, sz_dtype,
+                                 group_size, ngroups, N, nch, pitch, out, out_dtype); break;
+      case 3: hipLaunchKernelGGL(dequant_chunks_k<3>, dim3(blocks), dim3(256), 0, st, packed, scales, zeros, sz_dtype,
+                                 group_size, ngroups, N, nch, pitch, out, out_dtype); break;
+      case 2: hipLaunchKernelGGL(dequant_chunks_k<2>, dim3(blocks), dim3(256), 0, st, packed, scales, zeros, sz_dtype,
+                                 group_size, ngroups, N, nch, pitch, out, out_dtype); break;
+      default: hipLaunchKernelGGL(dequant_chunks_k<8>, dim3(blocks), dim3(256), 0, st, packed, scales, zeros,
+                                  sz_dtype, group_size, ngroups, N, nch, pitch, out, out_dtype); break;
+    }
+    return check_launch("dequant");
+  }
+  hipLaunchKernelGGL(dequant_k, dim3(blocks_for(N * K)), dim3(256), 0, st, packed, bits, scales, zeros, sz_dtype, g_idx,
+                     group_size, ngroups, N, K, out, out_dtype, pitch);
   return check_launch("dequant");
+}
+
+extern "C" int gptq_dequant(const uint8_t* packed, int bits, const void* scales, const void* zeros, int sz_dtype,
+                            const int32_t* g_idx, int group_size, int64_t ngroups, int64_t N, int64_t K, float* out,
+                            gptq_stream_t stream) {
+  return gptq_dequant_to(packed, bits, scales, zeros, sz_dtype, g_idx, group_size, ngroups, N, K, out, GPTQ_F32,
+                         stream);
 }
 
 extern "C" int gptq_quantize_tensor(const void* x, int dtype, int64_t n, int bits, int group_size, int flags,

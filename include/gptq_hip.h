@@ -196,6 +196,16 @@ int gptq_dequant(const uint8_t* packed, int bits, const void* scales,
                  int group_size, int64_t ngroups, int64_t N, int64_t K,
                  float* out, gptq_stream_t stream);
 
+/* gptq_dequant with W stored in out_dtype (GPTQ_F32, GPTQ_F16 or
+ * GPTQ_BF16): the fp32 value above rounded once to the output type, i.e. the
+ * weight the reference's fallback F.linear(x, unpack_weights(), bias)
+ * multiplies in x's dtype (models/layers.py:155-157).  Serves gptq::linear
+ * for many rows of x as this dequantisation plus a library GEMM. */
+int gptq_dequant_to(const uint8_t* packed, int bits, const void* scales,
+                    const void* zeros, int sz_dtype, const int32_t* g_idx,
+                    int group_size, int64_t ngroups, int64_t N, int64_t K,
+                    void* out, int out_dtype, gptq_stream_t stream);
+
 /* ------------------------------------------------ dequant GEMV / GEMM --
  * y[M x N] = x[M x K] @ W^T (+ bias), W as in gptq_dequant, fp32
  * accumulation, x/y in x_dtype (fp16, bf16 or fp32), bias (N) in bias_dtype

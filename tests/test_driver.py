@@ -438,6 +438,36 @@ def test_find_blocks_and_capture_inputs():
     assert torch.equal(out[0], m.blocks[0].lin(m.emb(data[0])) * 2.0)
 
 
+def test_group_plan_and_stop_hooks():
+    """The pieces of the true-sequential passes, on the CPU: the group order
+    learnt from a pass, and hooks that end a forward once a group has run."""
+    from distributed_gptq_amd.core import quantizer as Q
+    blk = Tiny(seed=1, d=32, f=64).layers[0]
+    names = {n: getattr(blk, n) for n in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj",
+                                          "down_proj")}
+    dq = Q.DistributedGPTQuantizer(Q.QuantizationConfig(), device="cpu")
+    dq._call_order = ["layers.0." + n for n in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj",
+                                                 "down_proj")]
+    groups = {0: ["layers.0.o_proj"], 1: ["layers.0.v_proj", "layers.0.q_proj", "layers.0.k_proj"],
+              2: ["layers.0.down_proj"], 3: ["layers.0.up_proj", "layers.0.gate_proj"]}
+    assert dq._group_plan(groups, "layers.0.") == [["q_proj", "k_proj", "v_proj"], ["o_proj"],
+                                                   ["gate_proj", "up_proj"], ["down_proj"]]
+    dq._call_order = dq._call_order[:-1]  # down_proj never reached: no plan
+    assert dq._group_plan(groups, "layers.0.") is None
+    seen = []
+    rec = [m.register_forward_hook(lambda m, i, o, n=n: seen.append(n)) for n, m in names.items()]
+    stop = dq._stop_hooks({n: names[n] for n in ("gate_proj", "up_proj")})
+    x = torch.randn(2, 5, 32)
+    for _ in range(2):  # the hooks reset between forwards
+        seen.clear()
+        with pytest.raises(Q._StopForward):
+            blk(x)
+        assert seen == ["q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj"]
+    for h in rec + stop:
+        h.remove()
+    blk(x)
+
+
 def _manual_sequential(base, data, bits, gs, actorder, true_seq):
     """The definition, step by step: per block of Tiny, per layer group in
     forward order (all seven at once without true_seq), one GPTQ per layer
@@ -488,9 +518,17 @@ def test_block_sequential_matches_manual_definition(hip, true_seq, bits, gs, act
     cfg = QuantizationConfig(bits=bits, group_size=gs, actorder=actorder, true_sequential=true_seq)
     model = copy.deepcopy(base)
     calls = []
+    # forwards reaching each block's down_proj before it is quantized: with
+    # true_seq the first block's group order is learnt from one full pass;
+    # afterwards a group's pass stops after its last layer, so the second
+    # block's down_proj runs only in its own pass
+    ran = {0: 0, 1: 0}
+    for b in (0, 1):
+        model.layers[b].down_proj.register_forward_hook(lambda *a, b=b: ran.__setitem__(b, ran[b] + 1))
     DistributedGPTQuantizer(cfg).quantize_model(model, data, blockwise=True,
                                                 progress_callback=lambda *a: calls.append(a[2]))
     assert len(calls) == 14 and len(set(calls)) == 14
+    assert ran == ({0: 2 * len(data), 1: len(data)} if true_seq else {0: len(data), 1: len(data)}), ran
     ref = _manual_sequential(base, data, bits, gs, actorder, true_seq)
     mods, rmods = dict(model.named_modules()), dict(ref.named_modules())
     for n, m in rmods.items():

@@ -50,6 +50,64 @@ def test_dequant_bit_exact(hip, bits, sdt):
     assert torch.equal(out.cpu(), tref)
 
 
+@pytest.mark.parametrize("bits", [0, 2, 3, 4, 8])
+@pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("K,gs,gidx", [(384, 128, False), (1024, 32, False), (200, 64, False), (256, 128, True)])
+def test_dequant_typed_bit_exact(hip, bits, odt, K, gs, gidx):
+    """Dequantised weights in fp16 / bf16 / fp32: the fp32 value rounded once
+    (torch's own rounding), on the 32-code chunk kernel (K % 32 == 0, groups
+    of a multiple of 32) and the per-element one (K = 200, g_idx)."""
+    from distributed_gptq_amd import _ops
+    rng = np.random.default_rng(bits + K)
+    N = 40
+    eb = 8 if bits == 0 else bits
+    ng = -(-K // gs)
+    codes = rng.integers(0, 2 ** eb, (N, K)).astype(np.uint8)
+    scales = torch.from_numpy(rng.uniform(1e-3, 1e-2, (N, ng))).half()
+    zeros = torch.from_numpy(rng.integers(0, 2 ** eb, (N, ng)).astype(np.float64) + 0.5).half()
+    g_idx = rng.permutation(np.arange(K) // gs) if gidx else np.arange(K) // gs
+    packed = codes if bits == 0 else O.pack_bitstream(codes, bits)
+    out = _ops.dequant(torch.from_numpy(packed).cuda(), bits, scales.cuda(), zeros.cuda(), K,
+                       g_idx=torch.from_numpy(g_idx).cuda() if gidx else None, group_size=gs, dtype=odt)
+    assert out.dtype == odt
+    ref = torch.from_numpy(O.dequant(codes, scales.float().numpy(), zeros.float().numpy(), g_idx)).to(odt)
+    assert torch.equal(out.cpu(), ref)
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,N,actorder", [(384, 96, True), (400, 1024, True), (2048, 640, False),
+                                          (3, 1024, True)])
+def test_quantized_linear_many_rows(hip, xdt, M, N, actorder):
+    """From DEQUANT_GEMM_ROWS rows of x the operator dequantises the weights
+    to x's dtype once and runs the library GEMM (act-order: x's columns
+    gathered when it has fewer rows than W, W's columns scattered otherwise);
+    both agree with the oracle, and with the fused kernels below the
+    threshold."""
+    from distributed_gptq_amd.models import layers as Lm
+    K, gs, bits = 512, 128, 4
+    rng = np.random.default_rng(M + N)
+    codes = rng.integers(0, 16, (N, K)).astype(np.uint8)
+    perm = rng.permutation(K) if actorder else np.arange(K)
+    g_idx = np.empty(K, np.int64)
+    g_idx[perm] = np.arange(K) // gs  # column perm[j] sits at sweep position j
+    scales = torch.from_numpy(rng.uniform(1e-3, 1e-2, (N, K // gs))).half()
+    zeros = torch.from_numpy(rng.integers(0, 16, (N, K // gs)).astype(np.float64)).half()
+    ql = Lm.QuantizedLinear(bits, gs, K, N, bias=True, packed=True).cuda()
+    ql.pack_weights(torch.from_numpy(codes).cuda(), scales.cuda(), zeros.cuda(), torch.from_numpy(g_idx).int().cuda(),
+                    perm=torch.from_numpy(perm).int().cuda() if actorder else None)
+    assert ql.perm.numel() == (K if actorder else 0)
+    with torch.no_grad():
+        ql.bias.copy_(torch.randn(N))
+    x = torch.randn(M, K, device="cuda").to(xdt)
+    with torch.no_grad():
+        y = ql(x)
+    assert y.dtype == xdt and y.shape == (M, N)
+    ref = O.linear(x.float().cpu().numpy(), codes, scales.numpy(), zeros.numpy(), g_idx,
+                   ql.bias.detach().float().cpu().numpy())
+    err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err < TOL[xdt], err
+
+
 def _case(M, N, K, bits, gs, seed, xdt):
     rng = np.random.default_rng(seed)
     codes = rng.integers(0, 2 ** bits, (N, K)).astype(np.uint8)
