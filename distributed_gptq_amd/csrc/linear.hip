@@ -1672,7 +1672,10 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
     return check_launch("dq_tile");
   }
   const int64_t t64 = cdiv(a.N, 64) * cdiv(a.M, 64);
-  if (t64 >= 192) {
+  // 64 < M <= 128 on 5120-row layers (160 tiles): the tiles measured 46 / 114 us
+  // against split-K's 84 / 206 us at 5120 x 5120 / 5120 x 13824 (M = 128);
+  // at 4096 rows (128 tiles) split-K stays as fast or faster
+  if (t64 >= 192 || (a.M > 64 && t64 >= 160)) {
     const dim3 grid(static_cast<unsigned>(cdiv(a.N, 64)), static_cast<unsigned>(cdiv(a.M, 64)));
     if (t64 <= 512) {
       hipLaunchKernelGGL((dq_tile_k<BITS, BF16, 64, 64, 128>), grid, dim3(256), 0, st, a);

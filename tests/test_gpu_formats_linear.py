@@ -292,6 +292,8 @@ def test_triton_quantized_linear(hip):
                                       # count) and with 64-column steps, 128-row tiles
                                       (40, 8200, 512, 128), (128, 8256, 384, 128), (64, 16448, 384, 128),
                                       (100, 16448, 640, 128), (130, 16448, 256, 128), (64, 32832, 256, 128),
+                                      # 64 < M <= 128 with 160-191 tiles (5120-row layers)
+                                      (96, 5121, 384, 128), (128, 5120, 640, 64),
                                       # split-K with 32-row M tiles; 64 x 64 tiles and split-K for M > 128
                                       (24, 4100, 1024, 128), (32, 1000, 512, 64), (160, 4100, 512, 128),
                                       (200, 2000, 512, 128)])
