@@ -331,6 +331,70 @@ def run_gemv(args, torch, dev, bits, M=1, min_bytes=1 << 30, reps=3, actorder=Fa
     return out, tot_b / tot_us * 1e-3
 
 
+def run_fused(args, torch, dev, bits=4, M=1, min_bytes=1 << 30, reps=3):
+    """Layers that share an input, as a decode step runs them: Llama-3-8B's
+    q/k/v (4096 + 1024 + 1024 rows) and gate/up (2 x 14336 rows) over K =
+    4096, once as separate gptq_linear launches and once as one launch over
+    the concatenated rows (FusedQuantizedLinear), inside a HIP graph,
+    rotating >= 1 GiB of weights."""
+    from distributed_gptq_amd import _ops
+    K = HID
+    out = {}
+    g = torch.Generator(device=dev).manual_seed(5)
+    for name, rows in (("qkv", [NQ * HD, NKV * HD, NKV * HD]), ("gate_up", [FFN, FFN])):
+        N = sum(rows)
+        nbytes = gemv_bytes(N, K, bits, M)
+        R = max(2, math.ceil(min_bytes / (N * K * bits // 8)))
+        codes = torch.randint(0, 2 ** bits, (N, K), generator=g, device=dev, dtype=torch.uint8)
+        q0 = _ops.pack(codes, bits)
+        qs = [q0.clone() for _ in range(R)]
+        sc = [(torch.rand(N, K // 128, generator=g, device=dev) * 9e-3 + 1e-3).half() for _ in range(R)]
+        zr = torch.full((N, K // 128), float(2 ** (bits - 1)), device=dev, dtype=torch.float16)
+        x = torch.randn(M, K, generator=g, device=dev, dtype=torch.float32).half()
+        y = torch.empty(M, N, device=dev, dtype=torch.float16)
+        offs = [sum(rows[:i]) for i in range(len(rows))]
+        # separate layers: row slices of the same buffers (contiguous views)
+        parts = [[(q[o:o + n], s_[o:o + n], zr[o:o + n], torch.empty(M, n, device=dev, dtype=torch.float16))
+                  for o, n in zip(offs, rows)] for q, s_ in zip(qs, sc)]
+        res = {}
+        for mode in ("separate", "fused"):
+            def body(r):
+                if mode == "fused":
+                    _ops.linear(x, qs[r], bits, sc[r], zr, K, group_size=128, out=y)
+                else:
+                    for (qp, sp, zp, yp) in parts[r]:
+                        _ops.linear(x, qp, bits, sp, zp, K, group_size=128, out=yp)
+            graph = torch.cuda.CUDAGraph()
+            st = torch.cuda.Stream()
+            st.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(st):
+                for r in range(R):
+                    body(r)
+                st.synchronize()
+                with torch.cuda.graph(graph, stream=st):
+                    for r in range(R):
+                        body(r)
+            torch.cuda.current_stream().wait_stream(st)
+            graph.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (reps * R)
+            res[mode] = {"us": round(us, 3), "GBps": round(nbytes / us * 1e-3, 1), "launches": 1 if mode == "fused"
+                         else len(rows)}
+            del graph
+        res["rows"] = rows
+        res["bytes"] = nbytes
+        out[name] = res
+        del qs, sc, parts
+        torch.cuda.empty_cache()
+    return out
+
+
 # ------------------------------------------------------------ CPU baseline --
 
 def _host_cpu():
@@ -672,6 +736,10 @@ def main():
             gm, _ = run_gemv(args, torch, dev, 4, M=M, actorder=True)
             result["gemv"][f"w4a16_actorder_m{M}"] = gm
             log(f"[bench] W4A16 act-order M={M}: {gm}")
+        # layers sharing an input in one launch (decode step, M = 1)
+        fu = run_fused(args, torch, dev)
+        result["gemv"]["w4a16_m1_shared_input"] = fu
+        log(f"[bench] W4A16 M=1 shared-input layers, separate vs one launch: {fu}")
     if args.no_block:
         result.setdefault("value", None)
     if not args.no_cpu:

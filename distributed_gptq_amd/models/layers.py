@@ -295,6 +295,52 @@ class QuantizedLinear(nn.Module):
         return q
 
 
+class FusedQuantizedLinear(nn.Module):
+    """Several QuantizedLinear layers that read the same input (q/k/v,
+    gate/up) served by one gptq::linear call: their weights, scales, zeros
+    and biases are concatenated along the output rows, so a decode step pays
+    one launch, and its fixed start-up cost, for all of them.  forward
+    returns one output per layer, in the order given.  The layers must agree
+    on in_features, bits, group size, storage and column order (g_idx and
+    perm): layers quantized against one shared Hessian do."""
+
+    def __init__(self, layers):
+        super().__init__()
+        layers = list(layers)
+        if not layers:
+            raise ValueError("FusedQuantizedLinear: no layers")
+        first = layers[0]
+        for q in layers[1:]:
+            same = (q.in_features == first.in_features and q.bits == first.bits
+                    and q.group_size == first.group_size and q.packed == first.packed
+                    and torch.equal(q.g_idx, first.g_idx) and torch.equal(q.perm, first.perm))
+            if not same:
+                raise ValueError("FusedQuantizedLinear: the layers differ in in_features, bits, group size, "
+                                 "storage or column order (g_idx / perm)")
+        self.bits, self.group_size, self.packed = first.bits, first.group_size, first.packed
+        self.in_features = first.in_features
+        self.splits = [q.out_features for q in layers]
+        self.out_features = sum(self.splits)
+        self.register_buffer("qweight", torch.cat([q.qweight for q in layers], 0))
+        self.register_buffer("scales", torch.cat([q.scales for q in layers], 0))
+        self.register_buffer("zeros", torch.cat([q.zeros for q in layers], 0))
+        self.register_buffer("g_idx", first.g_idx.clone())
+        self.register_buffer("perm", first.perm.clone())
+        if any(q.bias is not None for q in layers):
+            b = [q.bias.data if q.bias is not None else torch.zeros(q.out_features, device=q.qweight.device)
+                 for q in layers]
+            self.register_parameter("bias", nn.Parameter(torch.cat([t.float() for t in b], 0)))
+        else:
+            self.register_parameter("bias", None)
+
+    def forward(self, x: torch.Tensor):
+        if self.perm.numel():
+            y = torch.ops.gptq.linear(x, self.qweight, self.scales, self.zeros, self.g_idx, self.bias, self.perm)
+        else:
+            y = torch.ops.gptq.linear(x, self.qweight, self.scales, self.zeros, self.g_idx, self.bias)
+        return tuple(y.split(self.splits, dim=-1))
+
+
 def replace_with_quantized_layers(model: nn.Module, quantizers: dict, packed: bool = True) -> nn.Module:
     """models/layers.py:285-315: swap each quantized nn.Linear (by name) for a
     QuantizedLinear built from its GPTQ result."""

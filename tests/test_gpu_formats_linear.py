@@ -525,3 +525,43 @@ def test_quantized_linear_actorder_is_served_fast(hip, bits, gs, M):
     sd = {k: v for k, v in plain.state_dict().items() if k != "perm"}
     fresh.load_state_dict(sd)
     assert fresh.perm.numel() == 0 and torch.equal(fresh.qweight, plain.qweight)
+
+
+@pytest.mark.parametrize("M", [1, 16, 128, 512])
+@pytest.mark.parametrize("actorder", [False, True])
+def test_fused_quantized_linear(hip, M, actorder):
+    """Layers sharing an input in one call: each output equals its own
+    layer's (same oracle tolerance), for every kernel regime of M."""
+    from distributed_gptq_amd.models import layers as Lm
+    K, gs, bits = 512, 128, 4
+    rows = [256, 64, 64]
+    rng = np.random.default_rng(M + actorder)
+    perm = rng.permutation(K) if actorder else np.arange(K)
+    g_idx = np.empty(K, np.int64)
+    g_idx[perm] = np.arange(K) // gs
+    layers, refs = [], []
+    x = torch.randn(M, K, device="cuda").half()
+    for i, N in enumerate(rows):
+        codes = rng.integers(0, 16, (N, K)).astype(np.uint8)
+        scales = torch.from_numpy(rng.uniform(1e-3, 1e-2, (N, K // gs))).half()
+        zeros = torch.from_numpy(rng.integers(0, 16, (N, K // gs)).astype(np.float64)).half()
+        ql = Lm.QuantizedLinear(bits, gs, K, N, bias=i != 1, packed=True).cuda()
+        ql.pack_weights(torch.from_numpy(codes).cuda(), scales.cuda(), zeros.cuda(),
+                        torch.from_numpy(g_idx).int().cuda(),
+                        perm=torch.from_numpy(perm).int().cuda() if actorder else None)
+        if ql.bias is not None:
+            with torch.no_grad():
+                ql.bias.copy_(torch.randn(N))
+        layers.append(ql)
+        b = ql.bias.detach().float().cpu().numpy() if ql.bias is not None else None
+        refs.append(O.linear(x.float().cpu().numpy(), codes, scales.numpy(), zeros.numpy(), g_idx, b))
+    fused = Lm.FusedQuantizedLinear(layers)
+    assert fused.out_features == sum(rows) and fused.qweight.shape[0] == sum(rows)
+    with torch.no_grad():
+        ys = fused(x)
+        sep = [ql(x) for ql in layers]
+    assert len(ys) == 3
+    for y, y1, ref in zip(ys, sep, refs):
+        assert y.shape == y1.shape
+        err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+        assert err < TOL[torch.float16], err

@@ -72,3 +72,23 @@ def test_group_layout_resolution():
     g2[0] = 3
     gs, gi = _group_layout(g2, K, 4)
     assert gi is not None and int(gi[0]) == 3
+
+
+def test_fused_quantized_linear_rejects_mismatched_layers():
+    """Layers fused into one call must agree on in_features, bits, group
+    size, storage and column order."""
+    from distributed_gptq_amd.models.layers import FusedQuantizedLinear, QuantizedLinear
+    a = QuantizedLinear(4, 128, 256, 64, packed=True)
+    b = QuantizedLinear(4, 128, 256, 32, packed=True, bias=False)
+    f = FusedQuantizedLinear([a, b])
+    assert f.splits == [64, 32] and f.qweight.shape == (96, 128) and f.bias.shape == (96,)
+    with pytest.raises(ValueError):
+        FusedQuantizedLinear([a, QuantizedLinear(4, 64, 256, 32, packed=True)])
+    with pytest.raises(ValueError):
+        FusedQuantizedLinear([a, QuantizedLinear(3, 128, 256, 32, packed=True)])
+    c = QuantizedLinear(4, 128, 256, 32, packed=True)
+    c.perm = torch.arange(256, dtype=torch.int32).flip(0)
+    with pytest.raises(ValueError):
+        FusedQuantizedLinear([a, c])
+    with pytest.raises(ValueError):
+        FusedQuantizedLinear([])
