@@ -38,6 +38,7 @@ SIGNATURES = {
     "gptq_last_error": (ctypes.c_char_p, []),
     "gptq_abi_version": (_i, []),
     "gptq_hessian_workspace_size": (_sz, [_i64, _i64]),
+    "gptq_hessian_workspace_min": (_sz, [_i64]),
     "gptq_hessian_accumulate": (_i, [_p, _p, _i64, _i64, _i64, _i, _p, _sz, _p]),
     "gptq_factor_workspace_size": (_sz, [_i64]),
     "gptq_damp_factor": (_i, [_p, _i64, _f, _f, _p, _i, _p, _p, _p, _p, _p, _sz, _p]),

@@ -702,23 +702,15 @@ extern "C" size_t gptq_hessian_workspace_size(int64_t n, int64_t K) {
   return static_cast<size_t>(S) * ntiles * kTile * kTile * sizeof(float);
 }
 
-extern "C" int gptq_hessian_accumulate(float* H, const void* X, int64_t n, int64_t K, int64_t ldx, int dtype,
-                                       void* workspace, size_t workspace_bytes, gptq_stream_t stream) {
-  clear_error();
-  GPTQ_REQUIRE(H && (X || n == 0), GPTQ_ERR_ARG, "hessian_accumulate: null pointer");
-  GPTQ_REQUIRE(K > 0 && K <= (1 << 20) && n >= 0 && ldx >= K, GPTQ_ERR_SHAPE,
-               "hessian_accumulate: bad shape n=%lld K=%lld ldx=%lld", (long long)n, (long long)K, (long long)ldx);
-  GPTQ_REQUIRE(valid_dtype(dtype), GPTQ_ERR_DTYPE, "hessian_accumulate: bad dtype %d", dtype);
-  if (n == 0) return GPTQ_OK;
+namespace gptq {
+namespace {
+
+// H += X^T X for one run of tokens with S splits, partials in `part`
+int accumulate_run(float* H, const void* X, int64_t n, int64_t K, int64_t ldx, int dtype, int S, float* part,
+                   hipStream_t st) {
   const int64_t T = cdiv(K, kTile);
   const int ntiles = static_cast<int>(T * (T + 1) / 2);
-  const int S = choose_splits(n, ntiles);
-  const size_t need = static_cast<size_t>(S) * ntiles * kTile * kTile * sizeof(float);
-  GPTQ_REQUIRE(workspace && workspace_bytes >= need, GPTQ_ERR_WORKSPACE,
-               "hessian_accumulate: workspace %zu < %zu bytes", workspace_bytes, need);
   const int64_t per = cdiv(cdiv(n, S), 32) * 32;
-  float* part = static_cast<float*>(workspace);
-  hipStream_t st = as_hip(stream);
   const dim3 grid(static_cast<unsigned>(S) * ntiles);
   const int esz = dtype_size(dtype);
   const bool vec = (ldx * esz) % 16 == 0 && (reinterpret_cast<uintptr_t>(X) % 16) == 0 && (K * esz) % 16 == 0;
@@ -748,4 +740,47 @@ extern "C" int gptq_hessian_accumulate(float* H, const void* X, int64_t n, int64
   if (rc) return rc;
   hipLaunchKernelGGL(hessian_reduce, dim3(static_cast<unsigned>(ntiles) * 64), dim3(256), 0, st, H, (int)K, part, S, ntiles);
   return check_launch("hessian_reduce");
+}
+
+}  // namespace
+}  // namespace gptq
+
+extern "C" size_t gptq_hessian_workspace_min(int64_t K) {
+  if (K <= 0) return 0;
+  const int64_t T = cdiv(K, kTile);
+  return static_cast<size_t>(T * (T + 1) / 2) * kTile * kTile * sizeof(float);
+}
+
+extern "C" int gptq_hessian_accumulate(float* H, const void* X, int64_t n, int64_t K, int64_t ldx, int dtype,
+                                       void* workspace, size_t workspace_bytes, gptq_stream_t stream) {
+  clear_error();
+  GPTQ_REQUIRE(H && (X || n == 0), GPTQ_ERR_ARG, "hessian_accumulate: null pointer");
+  GPTQ_REQUIRE(K > 0 && K <= (1 << 20) && n >= 0 && ldx >= K, GPTQ_ERR_SHAPE,
+               "hessian_accumulate: bad shape n=%lld K=%lld ldx=%lld", (long long)n, (long long)K, (long long)ldx);
+  GPTQ_REQUIRE(valid_dtype(dtype), GPTQ_ERR_DTYPE, "hessian_accumulate: bad dtype %d", dtype);
+  if (n == 0) return GPTQ_OK;
+  const int64_t T = cdiv(K, kTile);
+  const int ntiles = static_cast<int>(T * (T + 1) / 2);
+  const size_t split_bytes = static_cast<size_t>(ntiles) * kTile * kTile * sizeof(float);
+  GPTQ_REQUIRE(workspace && workspace_bytes >= split_bytes, GPTQ_ERR_WORKSPACE,
+               "hessian_accumulate: workspace %zu < %zu bytes (one split's partial tiles)", workspace_bytes,
+               split_bytes);
+  float* part = static_cast<float*>(workspace);
+  hipStream_t st = as_hip(stream);
+  const int S = choose_splits(n, ntiles);
+  if (static_cast<size_t>(S) * split_bytes <= workspace_bytes)
+    return accumulate_run(H, X, n, K, ldx, dtype, S, part, st);
+  // a smaller workspace: consecutive runs of tokens, each with as many splits
+  // as the workspace holds, added to H one after the other (fixed order)
+  const int64_t cap = static_cast<int64_t>(workspace_bytes / split_bytes);
+  int64_t run = cap * 16384;
+  while (run > 1024 && choose_splits(run, ntiles) > cap) run /= 2;
+  const int esz = dtype_size(dtype);
+  for (int64_t t0 = 0; t0 < n; t0 += run) {
+    const int64_t m = std::min<int64_t>(run, n - t0);
+    const int Sm = static_cast<int>(std::min<int64_t>(choose_splits(m, ntiles), cap));
+    const int rc = accumulate_run(H, static_cast<const char*>(X) + t0 * ldx * esz, m, K, ldx, dtype, Sm, part, st);
+    if (rc) return rc;
+  }
+  return GPTQ_OK;
 }

@@ -55,6 +55,14 @@ int gptq_hessian_accumulate(float* H, const void* X, int64_t n, int64_t K,
                             int64_t ldx, int dtype, void* workspace,
                             size_t workspace_bytes, gptq_stream_t stream);
 
+/* The smallest workspace gptq_hessian_accumulate takes: one token split's
+ * partial tiles (ceil(K/256) (ceil(K/256) + 1) / 2 x 256 KB).  With less than
+ * gptq_hessian_workspace_size(n, K) the tokens are processed in consecutive
+ * runs, each with as many splits as the workspace holds, added to H in token
+ * order (deterministic; a little slower).  No counterpart in the reference
+ * (its add_batch allocates nothing beyond H); for callers short of memory. */
+size_t gptq_hessian_workspace_min(int64_t K);
+
 /* ------------------------------------------------------- damp + factorise --
  * Hd = scale * H[perm][:, perm] (perm may be NULL); if dead_cols is non-NULL,
  * every i with Hd[i][i] == 0 gets Hd[i][i] = 1 and dead_cols[i] = 1 (else 0);

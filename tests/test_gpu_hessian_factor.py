@@ -47,6 +47,37 @@ def test_hessian_many_splits(hip, dtype):
     assert torch.equal(H, H.T)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("cap_splits", [1, 3])
+def test_hessian_bounded_workspace(hip, dtype, cap_splits):
+    """A workspace of fewer token splits than the call would use: the tokens go
+    through in consecutive runs added to H in order; the result matches the
+    fp64 Gram matrix and, for 16-bit inputs, the one-run result to fp32
+    rounding; less than one split's partials is refused."""
+    from distributed_gptq_amd import _lib, _ops
+    n, K = 200000 + 17, 768
+    g = torch.Generator(device="cpu").manual_seed(cap_splits)
+    X = torch.randn(n, K, generator=g)
+    X[:, 5] *= 25
+    Xd = X.to(dtype).cuda()
+    lib = _lib.lib()
+    one = lib.gptq_hessian_workspace_min(K)
+    assert lib.gptq_hessian_workspace_size(n, K) > cap_splits * one
+    H = torch.zeros(K, K, device="cuda")
+    _ops.hessian_accumulate(H, Xd, workspace_cap=cap_splits * one)
+    Hfull = torch.zeros(K, K, device="cuda")
+    _ops.hessian_accumulate(Hfull, Xd)
+    Xn = Xd.double().cpu().numpy()
+    Href = Xn.T @ Xn
+    assert _rel(H.cpu().numpy(), Href) < 1e-5
+    assert torch.equal(H, H.T)
+    assert _rel(H.cpu().numpy(), Hfull.double().cpu().numpy()) < 1e-6
+    ws = torch.empty(one - 256, dtype=torch.uint8, device="cuda")
+    rc = lib.gptq_hessian_accumulate(_ops._p(H), _ops._p(Xd), n, K, K, _ops.dtype_code(dtype), _ops._p(ws),
+                                     ws.numel(), _ops._stream(H.device))
+    assert rc == _lib.ERR_WORKSPACE and b"one split" in lib.gptq_last_error()
+
+
 def test_hessian_accumulates_and_nonaligned_rows(hip):
     from distributed_gptq_amd import _ops
     K = 520
