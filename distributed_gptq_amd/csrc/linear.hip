@@ -1647,9 +1647,12 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
     // the register path stages the workgroup's scales and zeros in <= 64 KB of
     // LDS; 3-bit rows are read as dwords (the pitch must keep them aligned)
     if (a.M <= 16 && 64 * a.ngroups * sizeof(float2) <= 64 * 1024 && (BITS == 4 || a.pitch % 4 == 0)) {
-      // measured best per shape class (28672 x 4096, 14336 x 4096, 4096 x 14336)
+      // measured best per shape class (28672 x 4096, 14336 x 4096, 4096 x 14336;
+      // M <= 4 below 8192 rows: 16 waves, 6.7 / 15.8 us against 7.6 / 19.1 us
+      // at 4096 x 4096 / 4096 x 14336)
       if (a.N >= 64 * 256) return launch_reg4<BITS, 64, 4, BF16>(st, a);
       if (a.N >= 32 * 256) return launch_reg4<BITS, 64, 8, BF16>(st, a);
+      if (a.M <= 4) return launch_reg4<BITS, 16, 16, BF16>(st, a);
       return launch_reg4<BITS, 16, 8, BF16>(st, a);
     }
   }
