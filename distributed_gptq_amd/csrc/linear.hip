@@ -1017,6 +1017,25 @@ __device__ __forceinline__ void step_pairs(const uint32_t (&cw)[BITS], int kk, u
   }
 }
 
+// step_pairs without the final mask: word v >> 3t (3-bit) or >> 4t (4-bit),
+// whose low fields at bits 0 and 16 are the pair; the caller masks
+template <int BITS>
+__device__ __forceinline__ void step_fields(const uint32_t (&cw)[BITS], int kk, uint32_t (&p)[4]) {
+  if constexpr (BITS == 4) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) p[t] = cw[kk] >> (4 * t);
+  } else {
+    const uint32_t v = kk == 0 ? cw[0]
+                     : kk == 1 ? __builtin_amdgcn_alignbit(cw[1], cw[0], 24)
+                     : kk == 2 ? __builtin_amdgcn_alignbit(cw[2], cw[1], 16)
+                               : cw[2] >> 8;
+    // bits 3t..3t+2 -> 0..2 and 3t+12..3t+14 -> 16..18: the upper field moves
+    // 4 bits further than the lower one
+#pragma unroll
+    for (int t = 0; t < 4; ++t) p[t] = ((v >> (3 * t)) & 0x7u) | (((v >> (3 * t + 12)) & 0x7u) << 16);
+  }
+}
+
 __device__ __forceinline__ uint4 perm_0415(uint4 v) {
   return uint4{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
                __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
@@ -1047,10 +1066,10 @@ template <int BITS, int NT, int WAVES, bool kFold, bool BF16>
 __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
   constexpr int BN = NT / 16;
   __shared__ float red[WAVES][BN][4][64];
-  extern __shared__ float2 sz[];  // [NT][ngroups]: (scale, zero) of the workgroup's rows
+  extern __shared__ __attribute__((aligned(16))) float2 sz[];  // [ngroups][NT]: (scale, zero) of the workgroup's rows
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * NT;
   const int nblk = static_cast<int>(a.K / 128);
   const int r16 = lane & 15, g4 = lane >> 4;
@@ -1091,7 +1110,10 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
     uint4 xb[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) xb[kk] = xok ? perm_0415(L.x[kk]) : uint4{0u, 0u, 0u, 0u};
-    const int g = (b * 128 + 32 * g4) / a.gs;  // 32-bit division (K < 2^31)
+    // the lane's group: with groups of >= 128 columns the block's (one
+    // wave-uniform division), else per lane (32-bit division, K < 2^31)
+    const int g = kFold ? __builtin_amdgcn_readfirstlane(b * 128 / a.gs) : (b * 128 + 32 * g4) / a.gs;
+    const float2* szg = sz + g * NT;
     auto mfma = [](uint4 fa, uint4 fb, f32x4 c) {
       if constexpr (BF16)
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, fa), __builtin_bit_cast(bf16x8, fb),
@@ -1105,35 +1127,35 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
       constexpr uint32_t kOne = BF16 ? 0x3f803f80u : 0x3c003c00u;
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) sx = mfma(uint4{kOne, kOne, kOne, kOne}, xb[kk], sx);
-      const f16x2 magic = __builtin_bit_cast(f16x2, 0x64006400u);
-      constexpr float kZoff = BF16 ? 128.0f : 0.0f;
+      // the codes enter as 128 + q (bf16) or 1024 + q (fp16), both exact,
+      // straight from an AND-OR (the masks in registers let the compiler fuse
+      // the two), and the offset joins the zero in the correction
+      uint32_t mask = 0x000F000Fu, magic = BF16 ? 0x43004300u : 0x64006400u;
+      if constexpr (BITS == 3) mask = 0x00070007u;
+      asm volatile("" : "+v"(mask), "+v"(magic));
+      constexpr float kZoff = BF16 ? 128.0f : 1024.0f;
 #pragma unroll
       for (int i = 0; i < BN; ++i) {
         f32x4 t = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
           uint32_t q[4];
-          step_pairs<BITS>(L.cw[i], kk, q);
+          step_fields<BITS>(L.cw[i], kk, q);
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            if constexpr (BF16)
-              q[u] |= 0x43004300u;  // 128 + q
-            else
-              q[u] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, q[u] | 0x64006400u) - magic);
-          }
+          for (int u = 0; u < 4; ++u) q[u] = (q[u] & mask) | magic;
           t = mfma(uint4{q[0], q[1], q[2], q[3]}, xb[kk], t);
         }
+        const float4 p01 = *reinterpret_cast<const float4*>(szg + 16 * i + 4 * g4);
+        const float4 p23 = *reinterpret_cast<const float4*>(szg + 16 * i + 4 * g4 + 2);
+        const float ps[4] = {p01.x, p01.z, p23.x, p23.z}, pz[4] = {p01.y, p01.w, p23.y, p23.w};
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float2 p = sz[(16 * i + 4 * g4 + v) * ng + g];
-          acc[i][v] = fmaf(p.x, fmaf(-(p.y + kZoff), sx[v], t[v]), acc[i][v]);
-        }
+        for (int v = 0; v < 4; ++v) acc[i][v] = fmaf(ps[v], fmaf(-(pz[v] + kZoff), sx[v], t[v]), acc[i][v]);
       }
       return;
     }
 #pragma unroll
     for (int i = 0; i < BN; ++i) {
-      const float2 p = sz[(16 * i + r16) * ng + g];
+      const float2 p = szg[16 * i + r16];
       const float s = p.x, z = p.y;
       uint4 fa[4];
       uint32_t pr[4][4];
@@ -1168,7 +1190,7 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
   for (int e = tid; e < NT * ng; e += 64 * WAVES) {
     const int64_t n = std::min<int64_t>(n0 + e / ng, a.N - 1);
     const int64_t off = n * a.ngroups + e % ng;
-    sz[e] = float2{load_elem(a.scales, off, a.sz_dtype), load_elem(a.zeros, off, a.sz_dtype)};
+    sz[(e % ng) * NT + e / ng] = float2{load_elem(a.scales, off, a.sz_dtype), load_elem(a.zeros, off, a.sz_dtype)};
   }
   __syncthreads();
 
