@@ -55,6 +55,8 @@ SIGNATURES = {
     "gptq_dequant_to": (_i, [_p, _i, _p, _p, _i, _p, _i, _i64, _i64, _i64, _p, _i, _p]),
     "gptq_linear": (_i, [_p, _i, _i64, _p, _i, _p, _p, _i, _p, _i, _i64, _p, _i, _i64, _i64, _p, _p]),
     "gptq_linear_perm_workspace_size": (_sz, [_i64, _i64, _i]),
+    "gptq_linear_workspace_size": (_sz, [_i64, _i64, _i64, _i, _i, _i, _i]),
+    "gptq_linear_ws": (_i, [_p, _i, _i64, _p, _p, _i, _p, _p, _i, _p, _i, _i64, _p, _i, _i64, _i64, _p, _p, _sz, _p]),
     "gptq_linear_perm": (_i, [_p, _i, _i64, _p, _p, _i, _p, _p, _i, _p, _i, _i64, _p, _i, _i64, _i64, _p, _p, _sz,
                               _p]),
     "gptq_linear_perm_noalloc_max_bytes": (_sz, []),

@@ -273,19 +273,19 @@ def linear(x: torch.Tensor, packed: torch.Tensor, bits: int, scales: torch.Tenso
     if bias is not None:
         bias = bias.contiguous()
     y = out if out is not None else torch.empty((M, N), dtype=x.dtype, device=x.device)
-    if perm is None:
-        L.call("gptq_linear", _p(x2), dtype_code(x2.dtype), M, _p(packed), bits, _p(scales), _p(zeros),
-               dtype_code(scales.dtype), _p(g_idx), group_size, scales.shape[1], _p(bias),
-               dtype_code(bias.dtype) if bias is not None else 0, N, K, _p(y), _stream(x.device))
-        return y.reshape(*lead, N)
-    perm = perm.to(device=x.device, dtype=torch.int32).contiguous()
-    if perm.numel() != K:
-        raise ValueError(f"perm has {perm.numel()} entries, in_features is {K}")
-    nb = L.lib().gptq_linear_perm_workspace_size(M, K, dtype_code(x2.dtype))
-    ws = workspace(nb, x.device)
-    L.call("gptq_linear_perm", _p(x2), dtype_code(x2.dtype), M, _p(perm), _p(packed), bits, _p(scales), _p(zeros),
+    if perm is not None:
+        perm = perm.to(device=x.device, dtype=torch.int32).contiguous()
+        if perm.numel() != K:
+            raise ValueError(f"perm has {perm.numel()} entries, in_features is {K}")
+    # the gathered activations (act-order) and the split-K partial sums live
+    # in one workspace; exactly the requested size is passed, so the kernel
+    # choice depends on the shapes only
+    nb = L.lib().gptq_linear_workspace_size(M, N, K, bits, group_size if g_idx is None else 0,
+                                            dtype_code(x2.dtype), int(perm is not None))
+    ws = workspace(nb, x.device) if nb else None
+    L.call("gptq_linear_ws", _p(x2), dtype_code(x2.dtype), M, _p(perm), _p(packed), bits, _p(scales), _p(zeros),
            dtype_code(scales.dtype), _p(g_idx), group_size, scales.shape[1], _p(bias),
-           dtype_code(bias.dtype) if bias is not None else 0, N, K, _p(y), _p(ws), ws.numel(), _stream(x.device))
+           dtype_code(bias.dtype) if bias is not None else 0, N, K, _p(y), _p(ws), nb, _stream(x.device))
     return y.reshape(*lead, N)
 
 

@@ -22,8 +22,11 @@
 //    v_mfma_f32_16x16x32_{f16,bf16} (dq_split_k: the waves of a workgroup
 //    split K over 128-column blocks and reduce through LDS; dq_tile_k:
 //    128-row weight tiles x 64/128 activation rows, double-buffered LDS).
-//  * dq_rx_k (64 < M <= 128, wide layers): the codes are decoded in registers
-//    straight into the MFMA operands; X is staged in LDS by loader waves.
+//  * dq_rx_k (64 < M <= 128): the codes are decoded in registers straight
+//    into the MFMA operands; X is staged in LDS by loader waves.  Layers of
+//    fewer than 192 x 128 rows split K over workgroups when the caller gives
+//    a workspace for the fp32 partial sums (splitk_reduce_k adds them in
+//    split order).
 //  * dq_mfma_k (other M > 4 layouts): 16 weight rows x 16 activation rows per
 //    MFMA step with zero points folded per group, 4 waves splitting K.
 //  * linear_generic: any layout (fp32 x, g_idx, ragged K): one wave per
@@ -143,6 +146,8 @@ struct LinArgs {
   int64_t N, K;
   uint16_t* y;
   int y_dtype;
+  float* part = nullptr;      // split-K partial sums (fp32 [S][M][N]) or null
+  size_t part_bytes = 0;      // bytes available at part
 };
 
 constexpr int kRB = 4;  // weight rows per wave pass
@@ -1437,7 +1442,11 @@ __global__ __launch_bounds__(64 * (WAVES + L)) __attribute__((amdgpu_waves_per_e
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * MT;
-  const int nblk = static_cast<int>(a.K / 128);
+  // split-K: this workgroup's 128-column blocks kb0 .. kb0 + nblk - 1
+  const int ktot = static_cast<int>(a.K / 128);
+  const int bps = static_cast<int>(cdiv(ktot, gridDim.z));
+  const int kb0 = static_cast<int>(blockIdx.z) * bps;
+  const int nblk = std::min(ktot - kb0, bps);
   const int nsteps = static_cast<int>(cdiv(nblk, S)) * S;  // whole rounds of the S code slots
 
   if (wave >= WAVES) {
@@ -1453,7 +1462,7 @@ __global__ __launch_bounds__(64 * (WAVES + L)) __attribute__((amdgpu_waves_per_e
     auto load_x = [&](int b) {
 #pragma unroll
       for (int v = 0; v < XP; ++v) {
-        const uint32_t off = static_cast<uint32_t>((4 * L * v * a.K + static_cast<int64_t>(b) * 128) * 2);
+        const uint32_t off = static_cast<uint32_t>((4 * L * v * a.K + static_cast<int64_t>(kb0 + b) * 128) * 2);
         xr[v] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, voff + off, 0, 0));
       }
     };
@@ -1489,7 +1498,7 @@ __global__ __launch_bounds__(64 * (WAVES + L)) __attribute__((amdgpu_waves_per_e
   }
   using Cd = RxCodes<NW, BITS>;
   auto load_codes = [&](int b, Cd& C) {
-    const int64_t k = static_cast<int64_t>(b) * 128 + 32 * g4;
+    const int64_t k = static_cast<int64_t>(kb0 + b) * 128 + 32 * g4;
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const uint32_t* src = reinterpret_cast<const uint32_t*>(wrow[i] + k * BITS / 8);
@@ -1609,7 +1618,28 @@ __global__ __launch_bounds__(64 * (WAVES + L)) __attribute__((amdgpu_waves_per_e
   }
 
   // 16x16 layout: lane l, register v -> weight row 4 (l / 16) + v, X row l % 16;
-  // four consecutive outputs of a row go out as one 8-byte store
+  // four consecutive outputs of a row go out as one 8-byte store (split-K:
+  // fp32 partial sums, 16 bytes, without the bias)
+  if (gridDim.z > 1) {
+    float* part = a.part + static_cast<int64_t>(blockIdx.z) * a.M * a.N;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int64_t n = n0 + 16 * i + 4 * g4;
+#pragma unroll
+      for (int j = 0; j < MB; ++j) {
+        const int64_t m = m0 + 16 * j + r16;
+        if (m >= a.M) continue;
+        if (n + 3 < a.N && (a.N & 3) == 0) {
+          *reinterpret_cast<f32x4*>(part + m * a.N + n) = acc[i][j];
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (n + v < a.N) part[m * a.N + n + v] = acc[i][j][v];
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
     const int64_t n = n0 + 16 * i + 4 * g4;
@@ -1638,11 +1668,50 @@ __global__ __launch_bounds__(64 * (WAVES + L)) __attribute__((amdgpu_waves_per_e
   }
 }
 
+// y = bias + sum of the split-K partial sums, in split order (deterministic);
+// four outputs per thread
+__global__ __launch_bounds__(256) void splitk_reduce_k(const float* __restrict__ part, int S, int64_t M, int64_t N,
+                                                       const void* __restrict__ bias, int bias_dtype, void* y,
+                                                       int y_dtype) {
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t e = 4 * q;
+  if (e >= M * N) return;
+  const int64_t plane = M * N;
+  f32x4 v = *reinterpret_cast<const f32x4*>(part + e);
+  for (int s = 1; s < S; ++s) v += *reinterpret_cast<const f32x4*>(part + s * plane + e);
+  const int64_t n = e % N;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    float r = v[u];
+    if (bias) r += load_elem(bias, n + u, bias_dtype);
+    store_elem(y, e + u, y_dtype, r);
+  }
+}
+
 template <int BITS, bool BF16, int NW, int WAVES, int L, int MT, int S, int OCC>
-int launch_rx(hipStream_t st, const LinArgs& a) {
-  const dim3 grid(static_cast<unsigned>(cdiv(a.N, NW * WAVES)), static_cast<unsigned>(cdiv(a.M, MT)));
+int launch_rx(hipStream_t st, const LinArgs& a, int splits = 1) {
+  const dim3 grid(static_cast<unsigned>(cdiv(a.N, NW * WAVES)), static_cast<unsigned>(cdiv(a.M, MT)),
+                  static_cast<unsigned>(splits));
   hipLaunchKernelGGL((dq_rx_k<BITS, BF16, NW, WAVES, L, MT, S, OCC>), grid, dim3(64 * (WAVES + L)), 0, st, a);
-  return check_launch("dq_rx");
+  int rc = check_launch("dq_rx");
+  if (rc != GPTQ_OK || splits == 1) return rc;
+  const int64_t quads = a.M * a.N / 4;
+  hipLaunchKernelGGL(splitk_reduce_k, dim3(static_cast<unsigned>(cdiv(quads, 256))), dim3(256), 0, st, a.part, splits,
+                     a.M, a.N, a.bias, a.bias_dtype, static_cast<void*>(a.y), a.y_dtype);
+  return check_launch("splitk_reduce");
+}
+
+// split-K factor of the register-decoded kernel for 64 < M <= 128: enough
+// K splits that the 128-row workgroups cover every CU (1 on layers of >= 192
+// workgroups); 0 when the layout does not take it
+inline int rx_splits(const LinArgs& a, int bits) {
+  if (!((bits == 4 || bits == 3) && a.M > 64 && a.M <= 128 && (bits == 4 || a.pitch % 4 == 0))) return 0;
+  const int64_t wgs = cdiv(a.N, 128), nblk = a.K / 128;
+  if (wgs >= 192) return 1;
+  int64_t s = std::min<int64_t>(nblk, std::max<int64_t>(1, 256 / wgs));
+  s = cdiv(nblk, cdiv(nblk, s));  // no empty split
+  if (s < 2 || a.N % 4 != 0) return 0;
+  return static_cast<int>(s);
 }
 
 template <int BITS, bool BF16, int NT, int MT, int WAVES>
@@ -1683,8 +1752,12 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
     // register-decoded kernel, one workgroup per CU (measured on MI355X at
     // 28672 x 4096, M = 128: 69 against 98 us (4-bit), 71 against 116 us
     // (3-bit); at M = 64 and on narrower layers the tile kernels are faster)
-    if (a.M > 64 && a.M <= 128 && a.N >= 192 * 128 && (BITS == 4 || a.pitch % 4 == 0))
-      return launch_rx<BITS, BF16, 16, 8, 2, 128, 4, 2>(st, a);
+    const int sp = rx_splits(a, BITS);
+    if (sp == 1) return launch_rx<BITS, BF16, 16, 8, 2, 128, 4, 2>(st, a);
+    // narrower layers with the caller's workspace: K split over workgroups
+    // so that about 256 of them run, fp32 partial sums reduced in split order
+    if (sp > 1 && a.part && static_cast<size_t>(sp) * a.M * a.N * sizeof(float) <= a.part_bytes)
+      return launch_rx<BITS, BF16, 16, 8, 2, 128, 4, 2>(st, a, sp);
   }
   if (a.M <= 16) {
     if (a.N >= 64 * 256) return launch_split<BITS, BF16, 64, 16, 8>(st, a);
@@ -1919,6 +1992,67 @@ extern "C" int gptq_linear(const void* x, int x_dtype, int64_t M, const uint8_t*
 extern "C" size_t gptq_linear_perm_workspace_size(int64_t M, int64_t K, int x_dtype) {
   if (M <= 0 || K <= 0 || !valid_dtype(x_dtype)) return 0;
   return static_cast<size_t>(M) * static_cast<size_t>(K) * static_cast<size_t>(dtype_size(x_dtype));
+}
+
+namespace gptq {
+namespace {
+
+size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+
+// split-K partial-sum bytes the register-decoded kernel would use for this
+// layer (0 when it does not split)
+size_t splitk_bytes(int64_t M, int64_t N, int64_t K, int bits, int group_size, int x_dtype) {
+  if (M <= 0 || N <= 0 || K <= 0 || x_dtype == GPTQ_F32 || K % 128 != 0 || group_size <= 0 || group_size % 32 != 0)
+    return 0;
+  LinArgs a{};
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.pitch = (K * bits + 7) / 8;
+  const int sp = rx_splits(a, bits);
+  return sp > 1 ? static_cast<size_t>(sp) * M * N * sizeof(float) : 0;
+}
+
+}  // namespace
+}  // namespace gptq
+
+extern "C" size_t gptq_linear_workspace_size(int64_t M, int64_t N, int64_t K, int bits, int group_size, int x_dtype,
+                                             int has_perm) {
+  if (M <= 0 || N <= 0 || K <= 0 || !valid_dtype(x_dtype)) return 0;
+  const size_t gather = has_perm ? round256(static_cast<size_t>(M) * K * dtype_size(x_dtype)) : 0;
+  return gather + splitk_bytes(M, N, K, bits, group_size, x_dtype);
+}
+
+extern "C" int gptq_linear_ws(const void* x, int x_dtype, int64_t M, const int32_t* perm, const uint8_t* packed,
+                              int bits, const void* scales, const void* zeros, int sz_dtype, const int32_t* g_idx,
+                              int group_size, int64_t ngroups, const void* bias, int bias_dtype, int64_t N, int64_t K,
+                              void* y, void* workspace, size_t workspace_bytes, gptq_stream_t stream) {
+  clear_error();
+  const int rc = check_linear_args(x, x_dtype, M, packed, bits, scales, zeros, sz_dtype, g_idx, group_size, ngroups,
+                                   bias, bias_dtype, N, K, y);
+  if (rc != GPTQ_OK || M == 0) return rc;
+  hipStream_t st = as_hip(stream);
+  LinArgs a = make_linear_args(x, x_dtype, M, packed, bits, scales, zeros, sz_dtype, group_size, ngroups, bias,
+                               bias_dtype, N, K, y);
+  size_t used = 0;
+  if (perm) {
+    const size_t need = static_cast<size_t>(M) * K * dtype_size(x_dtype);
+    GPTQ_REQUIRE(workspace && workspace_bytes >= need, GPTQ_ERR_WORKSPACE,
+                 "linear_ws: workspace of %zu bytes, %zu needed for the gathered activations", workspace_bytes, need);
+    const dim3 grid(static_cast<unsigned>(cdiv(K, 256)), static_cast<unsigned>(std::min<int64_t>(M, 65535)));
+    hipLaunchKernelGGL(gather_cols_k, grid, dim3(256), 0, st, x, dtype_size(x_dtype), M, K, perm, workspace);
+    const int lrc = check_launch("gather_cols");
+    if (lrc != GPTQ_OK) return lrc;
+    a.x = static_cast<const uint16_t*>(workspace);
+    used = round256(need);
+  }
+  // the rest of the workspace holds split-K partial sums when the kernel
+  // takes them and they fit (else the layer runs unsplit)
+  if (workspace && workspace_bytes > used) {
+    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + used);
+    a.part_bytes = workspace_bytes - used;
+  }
+  return dispatch_linear(st, a, bits, g_idx);
 }
 
 extern "C" int gptq_linear_perm(const void* x, int x_dtype, int64_t M, const int32_t* perm, const uint8_t* packed,

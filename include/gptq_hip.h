@@ -227,6 +227,24 @@ int gptq_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packed,
                 const void* bias, int bias_dtype, int64_t N, int64_t K,
                 void* y, gptq_stream_t stream);
 
+/* gptq_linear with a caller workspace (perm may be NULL): with perm, x is
+ * gathered through it into the workspace first (as gptq_linear_perm); the
+ * rest of the workspace lets the M = 65..128 kernel split K over more
+ * workgroups on narrower layers, its fp32 partial sums reduced in split
+ * order (deterministic).  gptq_linear_workspace_size gives the bytes for
+ * both (has_perm: 0 or 1); with less, the layer runs as gptq_linear would.
+ * Same semantics as gptq_linear; no counterpart in the reference beyond
+ * torch.ops.gptq.linear (models/layers.py:151-157). */
+size_t gptq_linear_workspace_size(int64_t M, int64_t N, int64_t K, int bits,
+                                  int group_size, int x_dtype, int has_perm);
+int gptq_linear_ws(const void* x, int x_dtype, int64_t M, const int32_t* perm,
+                   const uint8_t* packed, int bits, const void* scales,
+                   const void* zeros, int sz_dtype, const int32_t* g_idx,
+                   int group_size, int64_t ngroups, const void* bias,
+                   int bias_dtype, int64_t N, int64_t K, void* y,
+                   void* workspace, size_t workspace_bytes,
+                   gptq_stream_t stream);
+
 /* y = x[:, perm] @ W^T (+ bias), W and the other arguments as in
  * gptq_linear: the act-order serving layout, where weight column j holds
  * input column perm[j] (perm: K int32, a permutation of [0, K); entries

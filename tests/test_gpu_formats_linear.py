@@ -340,6 +340,45 @@ def test_linear_register_decoded_wide(hip, xdt, bits, M, N, K, gs, zkind, sdt):
 
 
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bits", [3, 4])
+@pytest.mark.parametrize("M,N,K,gs,zkind,sdt,act", [
+    # 32 workgroups x 8 splits of 4 blocks
+    (128, 4096, 4096, 128, "int", torch.float16, False),
+    # ragged splits (11 blocks over 6 splits, the last one block), groups of 64
+    (100, 5120, 1408, 64, "int", torch.float16, False),
+    # one block per split, ragged last workgroup (N % 128 = 4), groups of 32
+    (65, 1028, 640, 32, "int", torch.float16, False),
+    # two splits; fractional zeros, fp32 scales; with act-order gather in front
+    (128, 14336, 1024, 128, "frac", torch.float32, True),
+    (96, 2048, 2048, 128, "int", torch.float16, True)])
+def test_linear_register_decoded_split_k(hip, xdt, bits, M, N, K, gs, zkind, sdt, act):
+    """64 < M <= 128 on layers of < 192 x 128 rows: the register-decoded
+    kernel with K split over workgroups (fp32 partials in the workspace,
+    reduced in split order, bias added there), against the fp64 oracle;
+    the same call twice gives identical bits."""
+    from distributed_gptq_amd import _lib, _ops
+    nb = _lib.lib().gptq_linear_workspace_size(M, N, K, bits, gs, _ops.dtype_code(xdt), int(act))
+    assert nb >= 2 * M * N * 4  # the split path is the one under test
+    codes, scales, zeros, x = _case(M, N, K, bits, gs, M + N + bits + K, xdt)
+    if zkind == "frac":
+        rng = np.random.default_rng(N + K)
+        zeros = torch.from_numpy(rng.uniform(0, 2 ** bits - 1, zeros.shape)).half()
+    scales, zeros = scales.to(sdt), zeros.to(sdt)
+    bias = torch.randn(N).to(xdt)
+    perm = torch.from_numpy(np.random.default_rng(K).permutation(K).astype(np.int32)) if act else None
+    packed = torch.from_numpy(O.pack_bitstream(codes, bits)).cuda()
+    args = (x.cuda(), packed, bits, scales.cuda(), zeros.cuda(), K)
+    kw = dict(group_size=gs, bias=bias.cuda(), perm=perm.cuda() if act else None)
+    y = _ops.linear(*args, **kw)
+    assert torch.equal(y, _ops.linear(*args, **kw))
+    xr = x.float().numpy()[:, perm.numpy()] if act else x.float().numpy()
+    ref = O.linear(xr, codes, scales.float().numpy(), zeros.float().numpy(), np.arange(K) // gs,
+                   bias.float().numpy())
+    err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err < TOL[xdt], err
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("M,N", [(1, 1030), (3, 1030), (16, 4101), (128, 8256)])
 def test_linear_scales_at_odd_offset(hip, xdt, M, N):
     """Scales and zeros whose base is 2 but not 4-byte aligned (a contiguous

@@ -35,16 +35,29 @@ def _case(M, N, K, bits, gs, seed, xdt):
     return x, perm, packed, scales, zeros, bias
 
 
+def _call_perm(lib, x, perm, packed, bits, scales, zeros, gs, bias, N, K, y):
+    from distributed_gptq_amd import _ops
+    P = ctypes.c_void_p
+    nb = lib.gptq_linear_perm_workspace_size(x.shape[0], K, _ops.dtype_code(x.dtype))
+    ws = torch.empty(nb, dtype=torch.uint8, device=x.device)
+    return lib.gptq_linear_perm(
+        P(x.data_ptr()), _ops.dtype_code(x.dtype), x.shape[0], P(perm.data_ptr()), P(packed.data_ptr()), bits,
+        P(scales.data_ptr()), P(zeros.data_ptr()), _ops.dtype_code(scales.dtype), None, gs, scales.shape[1],
+        P(bias.data_ptr()) if bias is not None else None, _ops.dtype_code(bias.dtype) if bias is not None else 0,
+        N, K, P(y.data_ptr()), P(ws.data_ptr()), nb, P(torch.cuda.current_stream().cuda_stream))
+
+
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
 def test_noalloc_matches_workspace_entry_point(hip, xdt):
-    from distributed_gptq_amd import _lib, _ops
+    from distributed_gptq_amd import _lib
     lib = _lib.lib()
     assert lib.gptq_linear_perm_noalloc_max_bytes() == 4 << 20
     # two calls in a row, the second with a smaller input, then M = 1 (the
     # fused-gather GEMV, no scratch) and M = 16 again
     for M, N, K, bits in [(128, 4096, 4096, 4), (16, 1000, 1024, 3), (1, 2048, 4096, 4), (16, 4101, 4096, 4)]:
         x, perm, packed, scales, zeros, bias = _case(M, N, K, bits, 128, M + N, xdt)
-        ref = _ops.linear(x, packed, bits, scales, zeros, K, group_size=128, bias=bias, perm=perm)
+        ref = torch.empty(M, N, dtype=xdt, device="cuda")
+        assert _call_perm(lib, x, perm, packed, bits, scales, zeros, 128, bias, N, K, ref) == 0
         y = torch.empty(M, N, dtype=xdt, device="cuda")
         assert _call_noalloc(lib, x, perm, packed, bits, scales, zeros, 128, bias, N, K, y) == 0
         torch.cuda.synchronize()
