@@ -22,7 +22,7 @@
 //    v_mfma_f32_16x16x32_{f16,bf16} (dq_split_k: the waves of a workgroup
 //    split K over 128-column blocks and reduce through LDS; dq_tile_k:
 //    128-row weight tiles x 64/128 activation rows, double-buffered LDS).
-//  * dq_rx_k (64 < M <= 128): the codes are decoded in registers straight
+//  * dq_rx_k (16 < M <= 128): the codes are decoded in registers straight
 //    into the MFMA operands; X is staged in LDS by loader waves.  Layers of
 //    fewer than 192 x 128 rows split K over workgroups when the caller gives
 //    a workspace for the fp32 partial sums (splitk_reduce_k adds them in
@@ -1410,9 +1410,10 @@ __global__ __launch_bounds__(256) void dq_tile_k(LinArgs a) {
       }
 }
 
-// Large products with 4- or 3-bit codes (M > 64, K % 128 == 0, group size %
-// 32 == 0, wide layers): the weights never pass through LDS.  A workgroup
-// owns NW * WAVES weight rows x MT activation rows over the whole of K, with
+// Products with 4- or 3-bit codes and 16 < M <= 128 (K % 128 == 0, group
+// size % 32 == 0): the weights never pass through LDS.  A workgroup owns
+// NW * WAVES weight rows x MT activation rows over its range of K (all of K,
+// or one of gridDim.z equal ranges of 128-column blocks), with
 // WAVES compute waves and L loader waves.  Per 128-column block the loaders
 // stage the workgroup's MT x 128 piece of X in LDS (double-buffered, each
 // 8-column piece permuted into the order the codes decode in) and every
@@ -1701,11 +1702,14 @@ int launch_rx(hipStream_t st, const LinArgs& a, int splits = 1) {
   return check_launch("splitk_reduce");
 }
 
-// split-K factor of the register-decoded kernel for 64 < M <= 128: enough
+// split-K factor of the register-decoded kernel for 16 < M <= 128: enough
 // K splits that the 128-row workgroups cover every CU (1 on layers of >= 192
-// workgroups); 0 when the layout does not take it
+// workgroups); 0 when the layout does not take it, and for M <= 32 on layers
+// of <= 2^24 weights (measured on MI355X at 4096 x 4096, M = 24 / 32:
+// dq_split_k 12.5 / 13.6 us against 15.4 / 15.9 us)
 inline int rx_splits(const LinArgs& a, int bits) {
-  if (!((bits == 4 || bits == 3) && a.M > 64 && a.M <= 128 && (bits == 4 || a.pitch % 4 == 0))) return 0;
+  if (!((bits == 4 || bits == 3) && a.M > 16 && a.M <= 128 && (bits == 4 || a.pitch % 4 == 0))) return 0;
+  if (a.M <= 32 && a.N * a.K <= (int64_t(1) << 24)) return 0;
   const int64_t wgs = cdiv(a.N, 128), nblk = a.K / 128;
   if (wgs >= 192) return 1;
   int64_t s = std::min<int64_t>(nblk, std::max<int64_t>(1, 256 / wgs));
@@ -1724,7 +1728,9 @@ int launch_split(hipStream_t st, const LinArgs& a) {
 
 // M <= 16: the register path (4/3-bit) or split-K with 16 waves, weight rows
 // per workgroup chosen so that the grid stays >= 256 workgroups while X is
-// re-read by fewer of them.  M > 16 (measured on MI355X at N x K = 28672 x
+// re-read by fewer of them.  16 < M <= 128 with 4/3-bit codes: the
+// register-decoded kernel where its layout and workspace allow.  Otherwise,
+// M > 16 (measured on MI355X at N x K = 28672 x
 // 4096, 14336 x 4096, 4096 x 14336 and 4096 x 4096, M = 32-128): 64 x 64
 // tiles when there are >= 192 of them (128-column steps up to 512 tiles;
 // beyond, 64-column steps, where two workgroups per CU pay, on 64 x 128
@@ -1748,16 +1754,20 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
     }
   }
   if constexpr (BITS == 4 || BITS == 3) {
-    // 64 < M <= 128 on wide layers (>= 192 workgroups of 128 rows): the
-    // register-decoded kernel, one workgroup per CU (measured on MI355X at
-    // 28672 x 4096, M = 128: 69 against 98 us (4-bit), 71 against 116 us
-    // (3-bit); at M = 64 and on narrower layers the tile kernels are faster)
+    // 16 < M <= 128: the register-decoded kernel with activation tiles of
+    // 32, 64 or 128 rows, unsplit on wide layers (>= 192 workgroups of 128
+    // weight rows), else with K split over workgroups so that about 256 of
+    // them run when the caller's workspace holds the fp32 partial sums.
+    // Measured on MI355X (4-bit, us; before: the tile and split kernels below):
+    // 28672 x 4096 at M = 128 / 64 / 32: 69 / 45 / 40 against 98 / 56 / 53;
+    // 4096 x 14336 at M = 128 / 64 / 32: 50 / 38 / 33 against 112 / 67 / 39;
+    // 14336 x 4096 at M = 128 / 64 / 32: 46 / 30 / 27 against 51 / 42 / 41.
     const int sp = rx_splits(a, BITS);
-    if (sp == 1) return launch_rx<BITS, BF16, 16, 8, 2, 128, 4, 2>(st, a);
-    // narrower layers with the caller's workspace: K split over workgroups
-    // so that about 256 of them run, fp32 partial sums reduced in split order
-    if (sp > 1 && a.part && static_cast<size_t>(sp) * a.M * a.N * sizeof(float) <= a.part_bytes)
+    if (sp == 1 || (sp > 1 && a.part && static_cast<size_t>(sp) * a.M * a.N * sizeof(float) <= a.part_bytes)) {
+      if (a.M <= 32) return launch_rx<BITS, BF16, 16, 8, 1, 32, 4, 2>(st, a, sp);
+      if (a.M <= 64) return launch_rx<BITS, BF16, 16, 8, 2, 64, 4, 2>(st, a, sp);
       return launch_rx<BITS, BF16, 16, 8, 2, 128, 4, 2>(st, a, sp);
+    }
   }
   if (a.M <= 16) {
     if (a.N >= 64 * 256) return launch_split<BITS, BF16, 64, 16, 8>(st, a);

@@ -56,7 +56,7 @@ def test_library_loads_and_reports_version():
     assert h.gptq_sweep_workspace_size(4096, 4096, 128) == 4096 * 512 * 4
     assert h.gptq_sweep_workspace_size(4096, 4096, 1024) == 4096 * 1024 * 4
     # linear: the act-order gather (rounded to 256 B) + split-K partials when
-    # 64 < M <= 128 on a layer of < 192 x 128 rows (4096 rows: 32 x 8 splits)
+    # 16 < M <= 128 on a layer of < 192 x 128 rows (4096 rows: 32 x 8 splits)
     bf16 = 2
     assert h.gptq_linear_workspace_size(128, 4096, 4096, 4, 128, bf16, 0) == 8 * 128 * 4096 * 4
     assert h.gptq_linear_workspace_size(100, 4096, 4096, 4, 128, bf16, 1) == \
@@ -64,7 +64,10 @@ def test_library_loads_and_reports_version():
     # 11 blocks of 128 over 6 splits at 5120 rows (40 workgroups)
     assert h.gptq_linear_workspace_size(128, 5120, 1408, 3, 64, bf16, 0) == 6 * 128 * 5120 * 4
     assert h.gptq_linear_workspace_size(128, 28672, 4096, 4, 128, bf16, 0) == 0   # 224 workgroups
-    assert h.gptq_linear_workspace_size(64, 4096, 4096, 4, 128, bf16, 0) == 0     # M <= 64
+    assert h.gptq_linear_workspace_size(64, 4096, 14336, 4, 128, bf16, 0) == 8 * 64 * 4096 * 4
+    assert h.gptq_linear_workspace_size(17, 4096, 14336, 3, 128, bf16, 0) == 8 * 17 * 4096 * 4
+    assert h.gptq_linear_workspace_size(32, 4096, 4096, 4, 128, bf16, 0) == 0     # M <= 32 on 2^24 weights
+    assert h.gptq_linear_workspace_size(16, 4096, 14336, 4, 128, bf16, 0) == 0    # M <= 16
     assert h.gptq_linear_workspace_size(128, 4098, 4096, 4, 128, bf16, 0) == 0    # N % 4
     assert h.gptq_linear_workspace_size(128, 4096, 4096, 8, 128, bf16, 0) == 0    # 8-bit
     assert h.gptq_linear_workspace_size(16, 4096, 4096, 4, 128, bf16, 1) == 16 * 4096 * 2

@@ -299,15 +299,30 @@ def test_triton_quantized_linear(hip):
                                       (200, 2000, 512, 128)])
 def test_linear_dequant_gemm(hip, xdt, bits, M, N, K, gs):
     """M > 4: dequantise-then-MFMA kernels (split-K and tiled), ragged N and M,
-    groups of 32-128 (one group per 32-code chunk), bias."""
+    groups of 32-128 (one group per 32-code chunk), bias; through
+    gptq_linear_ws (_ops.linear) and through gptq_linear, which has no
+    workspace and so runs these kernels where the other takes the split
+    register-decoded one."""
     from distributed_gptq_amd import _ops
     codes, scales, zeros, x = _case(M, N, K, bits, gs, M + N + bits, xdt)
     bias = torch.randn(N).to(xdt)
     packed = torch.from_numpy(O.pack_bitstream(codes, bits)).cuda()
-    y = _ops.linear(x.cuda(), packed, bits, scales.cuda(), zeros.cuda(), K, group_size=gs, bias=bias.cuda())
+    args = (x.cuda(), packed, bits, scales.cuda(), zeros.cuda(), K)
     ref = O.linear(x.float().numpy(), codes, scales.numpy(), zeros.numpy(), np.arange(K) // gs, bias.float().numpy())
-    err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
-    assert err < TOL[xdt], err
+    for y in (_ops.linear(*args, group_size=gs, bias=bias.cuda()), _linear_plain(*args, gs, bias.cuda())):
+        err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+        assert err < TOL[xdt], err
+
+
+def _linear_plain(x, packed, bits, scales, zeros, K, gs, bias):
+    """gptq_linear through the C ABI (no workspace)."""
+    from distributed_gptq_amd import _lib, _ops
+    M, N = x.shape[0], scales.shape[0]
+    y = torch.empty(M, N, dtype=x.dtype, device=x.device)
+    _lib.call("gptq_linear", x.data_ptr(), _ops.dtype_code(x.dtype), M, packed.data_ptr(), bits, scales.data_ptr(),
+              zeros.data_ptr(), _ops.dtype_code(scales.dtype), None, gs, scales.shape[1], bias.data_ptr(),
+              _ops.dtype_code(bias.dtype), N, K, y.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    return y
 
 
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
@@ -320,9 +335,14 @@ def test_linear_dequant_gemm(hip, xdt, bits, M, N, K, gs):
     (65, 24578, 256, 32, "int", torch.float16),
     # zeros that are not integers (the fp32 decode for fp16 activations) and fp32 scales
     (128, 24576, 640, 128, "frac", torch.float16),
-    (128, 24576, 1152, 128, "int", torch.float32)])
+    (128, 24576, 1152, 128, "int", torch.float32),
+    # 64- and 32-row activation tiles
+    (64, 24576, 512, 128, "frac", torch.float16),
+    (33, 24580, 384, 64, "int", torch.float16),
+    (32, 24576, 768, 128, "int", torch.float32),
+    (20, 24578, 1024, 32, "int", torch.float16)])
 def test_linear_register_decoded_wide(hip, xdt, bits, M, N, K, gs, zkind, sdt):
-    """64 < M <= 128 on layers of >= 192 x 128 rows: the kernel that decodes
+    """16 < M <= 128 on layers of >= 192 x 128 rows: the kernel that decodes
     the codes in registers (loader waves stage X), against the fp64 oracle."""
     from distributed_gptq_amd import _ops
     codes, scales, zeros, x = _case(M, N, K, bits, gs, M + N + bits + K, xdt)
@@ -350,9 +370,14 @@ def test_linear_register_decoded_wide(hip, xdt, bits, M, N, K, gs, zkind, sdt):
     (65, 1028, 640, 32, "int", torch.float16, False),
     # two splits; fractional zeros, fp32 scales; with act-order gather in front
     (128, 14336, 1024, 128, "frac", torch.float32, True),
-    (96, 2048, 2048, 128, "int", torch.float16, True)])
+    (96, 2048, 2048, 128, "int", torch.float16, True),
+    # 64- and 32-row activation tiles (16 < M <= 64), ragged M
+    (64, 4096, 1024, 128, "int", torch.float16, False),
+    (50, 5120, 1408, 64, "frac", torch.float16, True),
+    (32, 2048, 8320, 128, "int", torch.float32, False),
+    (17, 1028, 17408, 32, "int", torch.float16, True)])
 def test_linear_register_decoded_split_k(hip, xdt, bits, M, N, K, gs, zkind, sdt, act):
-    """64 < M <= 128 on layers of < 192 x 128 rows: the register-decoded
+    """16 < M <= 128 on layers of < 192 x 128 rows: the register-decoded
     kernel with K split over workgroups (fp32 partials in the workspace,
     reduced in split order, bias added there), against the fp64 oracle;
     the same call twice gives identical bits."""
