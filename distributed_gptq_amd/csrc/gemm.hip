@@ -13,7 +13,12 @@
 // transposition is a compile-time parameter and the loads are branch-free
 // (see load_op).  Triangular operands
 // skip the k-tiles that are known to be zero; GEMM_C_LOWER skips tiles
-// strictly above the diagonal.
+// strictly above the diagonal.  With a single triangular flag the tiles are
+// dispatched heaviest first (the tiles with the longest k range, or only the
+// tiles on or below the diagonal for GEMM_C_LOWER), so that the grid does not
+// end on a few long tiles: measured on MI355X at 7168^3 (A = B = C = 7168^2)
+// 90.7 / 94.6 / 109.1 / 102.5 -> 117.9 / 116.4 / 115.7 / 110.5 TFLOP/s for
+// B <= j, B >= j, A <= i and C lower, with bit-identical results.
 #include "gemm.hpp"
 
 namespace gptq {
@@ -89,17 +94,51 @@ __device__ __forceinline__ void store_op(float* s, int tid, f32x4 (&pre)[TR * BK
   }
 }
 
+// dispatch order of the output tiles (workgroup index -> tile)
+enum TileOrder {
+  ORDER_ROWS = 0,       // row-major
+  ORDER_ROWS_DESC = 1,  // row-major, last tile row first (A <= i: work grows with i)
+  ORDER_COLS_DESC = 2,  // column-major, last tile column first (B <= j)
+  ORDER_COLS = 3,       // column-major (B >= j: work falls with j)
+  ORDER_LOWER = 4       // only tiles on or below the diagonal, row by row
+};
+
+template <int TM, int TN>
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int order, int& tm, int& tn) {
+  switch (order) {
+    case ORDER_ROWS_DESC: tm = tiles_m - 1 - bid / tiles_n; tn = bid % tiles_n; break;
+    case ORDER_COLS_DESC: tn = tiles_n - 1 - bid / tiles_m; tm = bid % tiles_m; break;
+    case ORDER_COLS: tn = bid / tiles_m; tm = bid % tiles_m; break;
+    case ORDER_LOWER: {
+      // tile row r holds c (r + 1) tiles (c = TM / TN), so it starts at
+      // c r (r + 1) / 2: r from the quadratic formula, then corrected
+      // exactly in integers
+      constexpr int c = TM / TN;
+      const float q = static_cast<float>(2 * bid) / c;
+      int r = static_cast<int>((sqrtf(1.0f + 4.0f * q) - 1.0f) * 0.5f);
+      r = r < 0 ? 0 : r;
+      while (c * (r + 1) * (r + 2) / 2 <= bid) ++r;
+      while (c * r * (r + 1) / 2 > bid) --r;
+      tm = r;
+      tn = bid - c * r * (r + 1) / 2;
+      break;
+    }
+    default: tm = bid / tiles_n; tn = bid % tiles_n; break;
+  }
+}
+
 template <int TM, int TN, int BK, bool kVec, bool kTA, bool kTB>
 __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(int64_t M, int64_t N, int64_t Kd, float alpha,
                                                            Operand a, Operand b, float beta, float* __restrict__ C,
-                                                           int64_t ldc, int flags, int tiles_n) {
+                                                           int64_t ldc, int flags, int tiles_m, int tiles_n,
+                                                           int order) {
   constexpr int P = BK + 2;
   constexpr int FM = TM / 64, FN = TN / 64;  // 32x32 blocks per wave
   constexpr int QA = TM * BK / 4 / kThreads, QB = TN * BK / 4 / kThreads;
   __shared__ float sA[TM * P];
   __shared__ float sB[TN * P];
-  const int tm = blockIdx.x / tiles_n;
-  const int tn = blockIdx.x % tiles_n;
+  int tm = 0, tn = 0;
+  tile_of<TM, TN>(static_cast<int>(blockIdx.x), tiles_m, tiles_n, order, tm, tn);
   const int64_t i0 = static_cast<int64_t>(tm) * TM;
   const int64_t j0 = static_cast<int64_t>(tn) * TN;
   if ((flags & GEMM_C_LOWER) && j0 > i0 + TM - 1) return;
@@ -201,10 +240,26 @@ struct GemmArgs {
 
 template <int TM, int TN, bool V, bool TA, bool TB>
 void launch_one(hipStream_t st, const GemmArgs& g) {
+  const int tiles_m = static_cast<int>(cdiv(g.M, TM));
   const int tiles_n = static_cast<int>(cdiv(g.N, TN));
-  const dim3 grid(static_cast<unsigned>(cdiv(g.M, TM) * tiles_n));
+  int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
+  int order = ORDER_ROWS;
+  switch (g.flags) {
+    case GEMM_KLIM_A_LE_I: order = ORDER_ROWS_DESC; break;
+    case GEMM_KLIM_B_LE_J: order = ORDER_COLS_DESC; break;
+    case GEMM_KLIM_B_GE_J: order = ORDER_COLS; break;
+    case GEMM_C_LOWER:
+      // square C whose tile rows hold exactly c (r + 1) tiles
+      if (g.M == g.N && (TM / TN) * tiles_m == tiles_n) {
+        order = ORDER_LOWER;
+        tiles = static_cast<int64_t>(TM / TN) * tiles_m * (tiles_m + 1) / 2;
+      }
+      break;
+    default: break;
+  }
+  const dim3 grid(static_cast<unsigned>(tiles));
   hipLaunchKernelGGL((gemm_f32_kernel<TM, TN, 32, V, TA, TB>), grid, dim3(kThreads), 0, st, g.M, g.N, g.Kd, g.alpha,
-                     g.a, g.b, g.beta, g.C, g.ldc, g.flags, tiles_n);
+                     g.a, g.b, g.beta, g.C, g.ldc, g.flags, tiles_m, tiles_n, order);
 }
 
 // transposition and vector width are compile-time in the kernel
