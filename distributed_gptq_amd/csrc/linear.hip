@@ -1918,7 +1918,9 @@ using namespace gptq;
 namespace gptq {
 namespace {
 
-// out[m][j] = x[m][perm[j]] (indices clamped to [0, K))
+// out[m][j] = x[m][perm[j]] (indices clamped to [0, K)).  One element per
+// thread: measured faster than 8 columns per thread with 16-byte stores,
+// whose grid is too small at M = 1 (7.0 against 7.9 us at K = 4096).
 __global__ __launch_bounds__(256) void gather_cols_k(const void* __restrict__ x, int esz, int64_t M, int64_t K,
                                                      const int32_t* __restrict__ perm, void* __restrict__ out) {
   const int64_t j = blockIdx.x * 256LL + threadIdx.x;
@@ -1930,6 +1932,11 @@ __global__ __launch_bounds__(256) void gather_cols_k(const void* __restrict__ x,
     else
       static_cast<uint16_t*>(out)[m * K + j] = static_cast<const uint16_t*>(x)[m * K + src];
   }
+}
+
+void launch_gather(hipStream_t st, const void* x, int esz, int64_t M, int64_t K, const int32_t* perm, void* out) {
+  const dim3 grid(static_cast<unsigned>(cdiv(K, 256)), static_cast<unsigned>(std::min<int64_t>(M, 65535)));
+  hipLaunchKernelGGL(gather_cols_k, grid, dim3(256), 0, st, x, esz, M, K, perm, out);
 }
 
 int check_linear_args(const void* x, int x_dtype, int64_t M, const uint8_t* packed, int bits, const void* scales,
@@ -2049,18 +2056,22 @@ extern "C" int gptq_linear_ws(const void* x, int x_dtype, int64_t M, const int32
     const size_t need = static_cast<size_t>(M) * K * dtype_size(x_dtype);
     GPTQ_REQUIRE(workspace && workspace_bytes >= need, GPTQ_ERR_WORKSPACE,
                  "linear_ws: workspace of %zu bytes, %zu needed for the gathered activations", workspace_bytes, need);
-    const dim3 grid(static_cast<unsigned>(cdiv(K, 256)), static_cast<unsigned>(std::min<int64_t>(M, 65535)));
-    hipLaunchKernelGGL(gather_cols_k, grid, dim3(256), 0, st, x, dtype_size(x_dtype), M, K, perm, workspace);
+    launch_gather(st, x, dtype_size(x_dtype), M, K, perm, workspace);
     const int lrc = check_launch("gather_cols");
     if (lrc != GPTQ_OK) return lrc;
     a.x = static_cast<const uint16_t*>(workspace);
     used = round256(need);
   }
-  // the rest of the workspace holds split-K partial sums when the kernel
-  // takes them and they fit (else the layer runs unsplit)
-  if (workspace && workspace_bytes > used) {
-    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + used);
-    a.part_bytes = workspace_bytes - used;
+  // the rest of the workspace, from its first 256-byte boundary, holds
+  // split-K partial sums when the kernel takes them and they fit (else the
+  // layer runs unsplit)
+  if (workspace) {
+    const uintptr_t base = reinterpret_cast<uintptr_t>(workspace);
+    const uintptr_t p0 = (base + used + 255) / 256 * 256;
+    if (p0 < base + workspace_bytes) {
+      a.part = reinterpret_cast<float*>(p0);
+      a.part_bytes = base + workspace_bytes - p0;
+    }
   }
   return dispatch_linear(st, a, bits, g_idx);
 }
@@ -2084,8 +2095,7 @@ extern "C" int gptq_linear_perm(const void* x, int x_dtype, int64_t M, const int
   const size_t need = gptq_linear_perm_workspace_size(M, K, x_dtype);
   GPTQ_REQUIRE(workspace && workspace_bytes >= need, GPTQ_ERR_WORKSPACE,
                "linear_perm: workspace of %zu bytes, %zu needed", workspace_bytes, need);
-  const dim3 grid(static_cast<unsigned>(cdiv(K, 256)), static_cast<unsigned>(std::min<int64_t>(M, 65535)));
-  hipLaunchKernelGGL(gather_cols_k, grid, dim3(256), 0, st, x, dtype_size(x_dtype), M, K, perm, workspace);
+  launch_gather(st, x, dtype_size(x_dtype), M, K, perm, workspace);
   const int lrc = check_launch("gather_cols");
   if (lrc != GPTQ_OK) return lrc;
   a.x = static_cast<const uint16_t*>(workspace);

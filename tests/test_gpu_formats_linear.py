@@ -403,6 +403,37 @@ def test_linear_register_decoded_split_k(hip, xdt, bits, M, N, K, gs, zkind, sdt
     assert err < TOL[xdt], err
 
 
+def test_linear_ws_workspace_alignment_and_size(hip):
+    """gptq_linear_ws with a workspace that starts 4 bytes past a 256-byte
+    boundary: the partial sums start at the next boundary, so the exact size
+    no longer fits and the layer runs unsplit (still correct); 256 bytes more
+    give the split result bit for bit.  No workspace at all runs unsplit."""
+    from distributed_gptq_amd import _lib, _ops
+    M, N, K, gs, bits, xdt = 128, 4096, 1024, 128, 4, torch.float16
+    codes, scales, zeros, x = _case(M, N, K, bits, gs, 11, xdt)
+    packed = torch.from_numpy(O.pack_bitstream(codes, bits)).cuda()
+    xc, sc, zc = x.cuda(), scales.cuda(), zeros.cuda()
+    nb = _lib.lib().gptq_linear_workspace_size(M, N, K, bits, gs, _ops.dtype_code(xdt), 0)
+    assert nb == 8 * M * N * 4
+    buf = torch.empty(nb + 1024, dtype=torch.uint8, device="cuda")
+    assert buf.data_ptr() % 256 == 0
+
+    def run(ws_ptr, ws_bytes):
+        y = torch.empty(M, N, dtype=xdt, device="cuda")
+        _lib.call("gptq_linear_ws", xc.data_ptr(), _ops.dtype_code(xdt), M, None, packed.data_ptr(), bits,
+                  sc.data_ptr(), zc.data_ptr(), _ops.dtype_code(sc.dtype), None, gs, sc.shape[1], None, 0, N, K,
+                  y.data_ptr(), ws_ptr, ws_bytes, torch.cuda.current_stream().cuda_stream)
+        return y
+
+    split = run(buf.data_ptr(), nb)
+    assert torch.equal(split, _ops.linear(xc, packed, bits, sc, zc, K, group_size=gs))
+    assert torch.equal(run(buf.data_ptr() + 4, nb + 256), split)
+    ref = O.linear(x.float().numpy(), codes, scales.numpy(), zeros.numpy(), np.arange(K) // gs)
+    for y in (run(buf.data_ptr() + 4, nb), run(None, 0)):
+        err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+        assert err < TOL[xdt], err
+
+
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("M,N", [(1, 1030), (3, 1030), (16, 4101), (128, 8256)])
 def test_linear_scales_at_odd_offset(hip, xdt, M, N):
@@ -522,13 +553,14 @@ def test_linear_perm_matches_oracle(hip, xdt, bits, M, N, K):
     assert err < TOL[xdt], err
 
 
-@pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
-def test_linear_perm_generic_and_fp32(hip, xdt):
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("K,gs", [(200, 50), (204, 51), (1003, 59)])
+def test_linear_perm_generic_and_fp32(hip, xdt, K, gs):
     """perm with layouts the fast kernels do not take (fp32 x; a g_idx that
-    stays out of order in the stored order): gather, then the generic
-    kernel."""
+    stays out of order in the stored order; K not a multiple of 8, where the
+    gather writes element by element): gather, then the generic kernel."""
     from distributed_gptq_amd import _ops
-    N, K, gs = 40, 200, 50
+    N = 40
     codes, scales, zeros, x = _case(5, N, K, 4, gs, 3, xdt)
     rng = np.random.default_rng(1)
     perm = rng.permutation(K).astype(np.int32)
