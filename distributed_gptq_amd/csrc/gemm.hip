@@ -5,7 +5,7 @@
 // (pitch BK + 2 floats: the two k-rows a 32x32x2 fragment reads land in
 // disjoint bank halves), next stage prefetched into registers while the
 // current one is multiplied.  Tiles are 128 x 64 (64 x 64 for products that
-// would give fewer than 256 such tiles), 32 deep: small tiles keep enough
+// would give fewer than 4096 such tiles), 32 deep: small tiles keep enough
 // waves resident per CU to hide the load latency of this single-buffered
 // pipeline, which measured faster than 128 x 128 or 256 x 128 tiles, and
 // than a double-buffered variant with one barrier per stage (fewer resident
@@ -292,7 +292,10 @@ int launch_gemm_f32(hipStream_t st, int64_t M, int64_t N, int64_t Kd, float alph
   const GemmArgs g{M, N, Kd, alpha, Operand{A, lda, transA, M}, Operand{B, ldb, !transB, N},  // B viewed as [j][k]
                    beta, C, ldc, flags};
   const bool vec = vec_ok(g.a, Kd) && vec_ok(g.b, Kd);
-  if (cdiv(M, 128) * cdiv(N, 64) < 256) return launch_tiles<64, 64>(st, g, vec);
+  // 64 x 64 tiles below 4096 tiles of 128 x 64 (measured on MI355X: the four
+  // triangular products at 3584^3 1.96 -> 1.76 ms, at 1792^3 0.42 -> 0.34 ms;
+  // at 7168^3 128 x 64 stays faster, 12.8 against 13.3 ms)
+  if (cdiv(M, 128) * cdiv(N, 64) < 4096) return launch_tiles<64, 64>(st, g, vec);
   return launch_tiles<128, 64>(st, g, vec);
 }
 
