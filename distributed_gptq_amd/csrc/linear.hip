@@ -1076,7 +1076,11 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * NT;
-  const int nblk = static_cast<int>(a.K / 128);
+  // split-K over grid.y: this workgroup's 128-column blocks kb0 .. kb0 + nblk - 1
+  const int ktot = static_cast<int>(a.K / 128);
+  const int bps = static_cast<int>(cdiv(ktot, gridDim.y));
+  const int kb0 = static_cast<int>(blockIdx.y) * bps;
+  const int nblk = std::min(ktot - kb0, bps);
   const int r16 = lane & 15, g4 = lane >> 4;
   const int ng = static_cast<int>(a.ngroups);
 
@@ -1092,7 +1096,7 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
   const uint16_t* xrow = a.x + (xok ? r16 : 0) * a.K;
 
   auto load = [&](int b, DrBlock<NT, BITS>& L) {
-    const int64_t k = static_cast<int64_t>(b) * 128 + 32 * g4;
+    const int64_t k = static_cast<int64_t>(kb0 + b) * 128 + 32 * g4;
 #pragma unroll
     for (int i = 0; i < BN; ++i) {
       const uint32_t* src = reinterpret_cast<const uint32_t*>(wrow[i] + k * BITS / 8);
@@ -1117,7 +1121,7 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
     for (int kk = 0; kk < 4; ++kk) xb[kk] = xok ? perm_0415(L.x[kk]) : uint4{0u, 0u, 0u, 0u};
     // the lane's group: with groups of >= 128 columns the block's (one
     // wave-uniform division), else per lane (32-bit division, K < 2^31)
-    const int g = kFold ? __builtin_amdgcn_readfirstlane(b * 128 / a.gs) : (b * 128 + 32 * g4) / a.gs;
+    const int g = kFold ? __builtin_amdgcn_readfirstlane((kb0 + b) * 128 / a.gs) : ((kb0 + b) * 128 + 32 * g4) / a.gs;
     const float2* szg = sz + g * NT;
     auto mfma = [](uint4 fa, uint4 fb, f32x4 c) {
       if constexpr (BF16)
@@ -1210,8 +1214,9 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
     b += WAVES;
   }
 
-  // partial tiles summed in wave order; 16x16 layout: lane l, register v ->
-  // W row 4 (l / 16) + v, X row l % 16
+  // partial tiles summed in wave order (then, split over grid.y, written as
+  // fp32 partial sums for splitk_reduce_k); 16x16 layout: lane l, register
+  // v -> W row 4 (l / 16) + v, X row l % 16
 #pragma unroll
   for (int i = 0; i < BN; ++i)
 #pragma unroll
@@ -1224,24 +1229,67 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
     for (int w = 0; w < WAVES; ++w) r += red[w][i][v][l];
     const int64_t m = l % 16, n = n0 + 16 * i + 4 * (l / 16) + v;
     if (m < a.M && n < a.N) {
-      if (a.bias) r += load_elem(a.bias, n, a.bias_dtype);
-      store_elem(a.y, m * a.N + n, a.y_dtype, r);
+      if (gridDim.y > 1) {
+        a.part[(blockIdx.y * a.M + m) * a.N + n] = r;
+      } else {
+        if (a.bias) r += load_elem(a.bias, n, a.bias_dtype);
+        store_elem(a.y, m * a.N + n, a.y_dtype, r);
+      }
     }
   }
 }
 
+// y = bias + sum of the split-K partial sums, in split order (deterministic);
+// four outputs per thread
+__global__ __launch_bounds__(256) void splitk_reduce_k(const float* __restrict__ part, int S, int64_t M, int64_t N,
+                                                       const void* __restrict__ bias, int bias_dtype, void* y,
+                                                       int y_dtype) {
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t e = 4 * q;
+  if (e >= M * N) return;
+  const int64_t plane = M * N;
+  f32x4 v = *reinterpret_cast<const f32x4*>(part + e);
+  for (int s = 1; s < S; ++s) v += *reinterpret_cast<const f32x4*>(part + s * plane + e);
+  const int64_t n = e % N;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    float r = v[u];
+    if (bias) r += load_elem(bias, n + u, bias_dtype);
+    store_elem(y, e + u, y_dtype, r);
+  }
+}
+
+// splits > 1: K split over grid.y, the fp32 partial sums in a.part (the
+// caller checked that they fit), then splitk_reduce_k
 template <int BITS, int NT, int WAVES, bool BF16>
-int launch_reg4(hipStream_t st, const LinArgs& a) {
+int launch_reg4(hipStream_t st, const LinArgs& a, int splits = 1) {
   const size_t lds = static_cast<size_t>(NT) * a.ngroups * sizeof(float2);
   // static partial-tile buffer + the staged scales and zeros within the CU's LDS
   GPTQ_REQUIRE(static_cast<size_t>(WAVES) * NT * 16 * sizeof(float) + lds <= 160 * 1024, GPTQ_ERR_SHAPE,
                "dq_reg4: %lld groups per row exceed the LDS budget", static_cast<long long>(a.ngroups));
-  const dim3 grid(static_cast<unsigned>(cdiv(a.N, NT)));
+  const dim3 grid(static_cast<unsigned>(cdiv(a.N, NT)), static_cast<unsigned>(splits));
   if (a.gs % 128 == 0)
     hipLaunchKernelGGL((dq_reg4_k<BITS, NT, WAVES, true, BF16>), grid, dim3(64 * WAVES), lds, st, a);
   else
     hipLaunchKernelGGL((dq_reg4_k<BITS, NT, WAVES, false, BF16>), grid, dim3(64 * WAVES), lds, st, a);
-  return check_launch("dq_reg4");
+  int rc = check_launch("dq_reg4");
+  if (rc != GPTQ_OK || splits == 1) return rc;
+  const int64_t quads = a.M * a.N / 4;
+  hipLaunchKernelGGL(splitk_reduce_k, dim3(static_cast<unsigned>(cdiv(quads, 256))), dim3(256), 0, st, a.part, splits,
+                     a.M, a.N, a.bias, a.bias_dtype, static_cast<void*>(a.y), a.y_dtype);
+  return check_launch("splitk_reduce");
+}
+
+// 4 < M <= 16 on layers of 4097-8191 rows: 32-row workgroups (160-255 of
+// them; 16-row ones would leave 64-127 CUs with two), and for K >= 8192 K
+// split in 3 when that keeps the grid within two workgroups per CU.
+// Measured on MI355X, 4-bit M = 16 (M = 8): 5120 x 5120 12.9 (11.1) us against
+// 16.0 (11.9) with 16-row workgroups, 5120 x 13824 split 24.5 (21.2) against
+// 37.2 (27.2), 6144 x 4096 11.0 (9.7) against 13.4 (10.2).  Returns the
+// split count, 0 outside these shapes.
+inline int reg4_mid_splits(const LinArgs& a) {
+  if (!(a.M > 4 && a.M <= 16 && a.N > 4096 && a.N < 8192)) return 0;
+  return a.K >= 8192 && 3 * cdiv(a.N, 32) <= 512 && a.N % 4 == 0 ? 3 : 1;
 }
 
 // Large products (M > 16 and enough output tiles): one workgroup per NT x MT
@@ -1669,26 +1717,6 @@ __global__ __launch_bounds__(64 * (WAVES + L)) __attribute__((amdgpu_waves_per_e
   }
 }
 
-// y = bias + sum of the split-K partial sums, in split order (deterministic);
-// four outputs per thread
-__global__ __launch_bounds__(256) void splitk_reduce_k(const float* __restrict__ part, int S, int64_t M, int64_t N,
-                                                       const void* __restrict__ bias, int bias_dtype, void* y,
-                                                       int y_dtype) {
-  const int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t e = 4 * q;
-  if (e >= M * N) return;
-  const int64_t plane = M * N;
-  f32x4 v = *reinterpret_cast<const f32x4*>(part + e);
-  for (int s = 1; s < S; ++s) v += *reinterpret_cast<const f32x4*>(part + s * plane + e);
-  const int64_t n = e % N;
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    float r = v[u];
-    if (bias) r += load_elem(bias, n + u, bias_dtype);
-    store_elem(y, e + u, y_dtype, r);
-  }
-}
-
 template <int BITS, bool BF16, int NW, int WAVES, int L, int MT, int S, int OCC>
 int launch_rx(hipStream_t st, const LinArgs& a, int splits = 1) {
   const dim3 grid(static_cast<unsigned>(cdiv(a.N, NW * WAVES)), static_cast<unsigned>(cdiv(a.M, MT)),
@@ -1749,6 +1777,10 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
       // at 4096 x 4096 / 4096 x 14336)
       if (a.N >= 64 * 256) return launch_reg4<BITS, 64, 4, BF16>(st, a);
       if (a.N >= 32 * 256) return launch_reg4<BITS, 64, 8, BF16>(st, a);
+      if (const int s = reg4_mid_splits(a)) {
+        const bool fits = a.part && static_cast<size_t>(s) * a.M * a.N * sizeof(float) <= a.part_bytes;
+        return launch_reg4<BITS, 32, 8, BF16>(st, a, s > 1 && fits ? s : 1);
+      }
       if (a.M <= 4) return launch_reg4<BITS, 16, 16, BF16>(st, a);
       return launch_reg4<BITS, 16, 8, BF16>(st, a);
     }
@@ -2026,7 +2058,9 @@ size_t splitk_bytes(int64_t M, int64_t N, int64_t K, int bits, int group_size, i
   a.N = N;
   a.K = K;
   a.pitch = (K * bits + 7) / 8;
-  const int sp = rx_splits(a, bits);
+  // M <= 16: the register path stages <= 128 groups per row
+  const int sp = M > 16 ? rx_splits(a, bits)
+                        : (bits == 4 || bits == 3) && cdiv(K, group_size) <= 128 ? reg4_mid_splits(a) : 0;
   return sp > 1 ? static_cast<size_t>(sp) * M * N * sizeof(float) : 0;
 }
 

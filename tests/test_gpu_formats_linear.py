@@ -403,6 +403,34 @@ def test_linear_register_decoded_split_k(hip, xdt, bits, M, N, K, gs, zkind, sdt
     assert err < TOL[xdt], err
 
 
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bits", [3, 4])
+@pytest.mark.parametrize("M,N,K,gs", [
+    (16, 5120, 13824, 128),   # 32-row workgroups, K in 3 ranges
+    (5, 5000, 8192, 64),      # ragged last workgroup, groups of 64 (per-weight dequantisation)
+    (9, 6144, 4096, 128),     # unsplit (K < 8192)
+    (12, 5122, 8320, 128)])   # N % 4 != 0: unsplit
+def test_linear_register_mid_rows(hip, xdt, bits, M, N, K, gs):
+    """4 < M <= 16 on layers of 4097-8191 rows: dq_reg4_k with 32-row
+    workgroups, split over K (partials reduced in order, bias added there)
+    when K >= 8192 and the workspace holds the partials; through
+    gptq_linear_ws and, unsplit, through gptq_linear; against the fp64
+    oracle."""
+    from distributed_gptq_amd import _lib, _ops
+    nb = _lib.lib().gptq_linear_workspace_size(M, N, K, bits, gs, _ops.dtype_code(xdt), 0)
+    assert nb == (3 * M * N * 4 if K >= 8192 and N % 4 == 0 else 0)
+    codes, scales, zeros, x = _case(M, N, K, bits, gs, M + N + K + bits, xdt)
+    bias = torch.randn(N).to(xdt)
+    packed = torch.from_numpy(O.pack_bitstream(codes, bits)).cuda()
+    args = (x.cuda(), packed, bits, scales.cuda(), zeros.cuda(), K)
+    ref = O.linear(x.float().numpy(), codes, scales.numpy(), zeros.numpy(), np.arange(K) // gs, bias.float().numpy())
+    y = _ops.linear(*args, group_size=gs, bias=bias.cuda())
+    assert torch.equal(y, _ops.linear(*args, group_size=gs, bias=bias.cuda()))
+    for out in (y, _linear_plain(*args, gs, bias.cuda())):
+        err = np.abs(out.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+        assert err < TOL[xdt], err
+
+
 def test_linear_ws_workspace_alignment_and_size(hip):
     """gptq_linear_ws with a workspace that starts 4 bytes past a 256-byte
     boundary: the partial sums start at the next boundary, so the exact size
