@@ -1280,15 +1280,16 @@ int launch_reg4(hipStream_t st, const LinArgs& a, int splits = 1) {
   return check_launch("splitk_reduce");
 }
 
-// 4 < M <= 16 on layers of 4097-8191 rows: 32-row workgroups (160-255 of
+// 1 < M <= 16 on layers of 4097-8191 rows: 32-row workgroups (160-255 of
 // them; 16-row ones would leave 64-127 CUs with two), and for K >= 8192 K
 // split in 3 when that keeps the grid within two workgroups per CU.
-// Measured on MI355X, 4-bit M = 16 (M = 8): 5120 x 5120 12.9 (11.1) us against
-// 16.0 (11.9) with 16-row workgroups, 5120 x 13824 split 24.5 (21.2) against
-// 37.2 (27.2), 6144 x 4096 11.0 (9.7) against 13.4 (10.2).  Returns the
-// split count, 0 outside these shapes.
+// Measured on MI355X, 4-bit M = 16 (M = 8; M = 2): 5120 x 5120 12.9 (11.1;
+// 10.2) us against 16.0 (11.9; 11.6) with 16-row workgroups, 5120 x 13824
+// split 24.5 (21.2; 20.0) against 37.2 (27.2; 22.1), 6144 x 4096 11.0 (9.7;
+// 9.1) against 13.4 (10.2; 9.7).  Returns the split count, 0 outside these
+// shapes.
 inline int reg4_mid_splits(const LinArgs& a) {
-  if (!(a.M > 4 && a.M <= 16 && a.N > 4096 && a.N < 8192)) return 0;
+  if (!(a.M > 1 && a.M <= 16 && a.N > 4096 && a.N < 8192)) return 0;
   return a.K >= 8192 && 3 * cdiv(a.N, 32) <= 512 && a.N % 4 == 0 ? 3 : 1;
 }
 

@@ -68,12 +68,13 @@ def test_library_loads_and_reports_version():
     assert h.gptq_linear_workspace_size(17, 4096, 14336, 3, 128, bf16, 0) == 8 * 17 * 4096 * 4
     assert h.gptq_linear_workspace_size(32, 4096, 4096, 4, 128, bf16, 0) == 0     # M <= 32 on 2^24 weights
     assert h.gptq_linear_workspace_size(16, 4096, 14336, 4, 128, bf16, 0) == 0    # M <= 16 at 4096 rows
-    # 4 < M <= 16 on 4097-8191 rows with K >= 8192: K in 3 ranges
+    # 1 < M <= 16 on 4097-8191 rows with K >= 8192: K in 3 ranges
     assert h.gptq_linear_workspace_size(16, 5120, 13824, 4, 128, bf16, 0) == 3 * 16 * 5120 * 4
     assert h.gptq_linear_workspace_size(5, 5120, 13824, 3, 128, bf16, 0) == 3 * 5 * 5120 * 4
     assert h.gptq_linear_workspace_size(5, 5120, 13824, 3, 32, bf16, 0) == 0      # > 128 groups
     assert h.gptq_linear_workspace_size(16, 5120, 5120, 4, 128, bf16, 0) == 0     # K < 8192
-    assert h.gptq_linear_workspace_size(4, 5120, 13824, 4, 128, bf16, 0) == 0     # M <= 4
+    assert h.gptq_linear_workspace_size(2, 5120, 13824, 4, 128, bf16, 0) == 3 * 2 * 5120 * 4
+    assert h.gptq_linear_workspace_size(1, 5120, 13824, 4, 128, bf16, 0) == 0     # M = 1: the GEMV
     assert h.gptq_linear_workspace_size(16, 5122, 13824, 4, 128, bf16, 0) == 0    # N % 4
     assert h.gptq_linear_workspace_size(128, 4098, 4096, 4, 128, bf16, 0) == 0    # N % 4
     assert h.gptq_linear_workspace_size(128, 4096, 4096, 8, 128, bf16, 0) == 0    # 8-bit

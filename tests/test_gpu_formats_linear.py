@@ -409,9 +409,10 @@ def test_linear_register_decoded_split_k(hip, xdt, bits, M, N, K, gs, zkind, sdt
     (16, 5120, 13824, 128),   # 32-row workgroups, K in 3 ranges
     (5, 5000, 8192, 64),      # ragged last workgroup, groups of 64 (per-weight dequantisation)
     (9, 6144, 4096, 128),     # unsplit (K < 8192)
-    (12, 5122, 8320, 128)])   # N % 4 != 0: unsplit
+    (12, 5122, 8320, 128),    # N % 4 != 0: unsplit
+    (2, 5120, 8192, 128), (3, 6148, 4096, 64)])
 def test_linear_register_mid_rows(hip, xdt, bits, M, N, K, gs):
-    """4 < M <= 16 on layers of 4097-8191 rows: dq_reg4_k with 32-row
+    """1 < M <= 16 on layers of 4097-8191 rows: dq_reg4_k with 32-row
     workgroups, split over K (partials reduced in order, bias added there)
     when K >= 8192 and the workspace holds the partials; through
     gptq_linear_ws and, unsplit, through gptq_linear; against the fp64
