@@ -1776,7 +1776,16 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
       // measured best per shape class (28672 x 4096, 14336 x 4096, 4096 x 14336;
       // M <= 4 below 8192 rows: 16 waves, 6.7 / 15.8 us against 7.6 / 19.1 us
       // at 4096 x 4096 / 4096 x 14336)
-      if (a.N >= 64 * 256) return launch_reg4<BITS, 64, 4, BF16>(st, a);
+      if (a.N >= 64 * 256) {
+        // 241-256 workgroups of 112 rows fill the CUs once where 64-row ones
+        // would leave a quarter of them with one workgroup and the rest with
+        // two (measured at 28672 x 4096, M = 16 / 8 / 2: 26.4 / 24.1 / 22.5 us
+        // against 26.8 / 25.1 / 23.6 (4-bit), 26.9 / 25.6 / 24.2 against
+        // 28.8 / 27.1 / 26.1 (3-bit))
+        const int64_t w112 = cdiv(a.N, 112);
+        if (w112 > 240 && w112 <= 256 && a.ngroups <= 64) return launch_reg4<BITS, 112, 8, BF16>(st, a);
+        return launch_reg4<BITS, 64, 4, BF16>(st, a);
+      }
       if (a.N >= 32 * 256) return launch_reg4<BITS, 64, 8, BF16>(st, a);
       if (const int s = reg4_mid_splits(a)) {
         const bool fits = a.part && static_cast<size_t>(s) * a.M * a.N * sizeof(float) <= a.part_bytes;

@@ -296,7 +296,9 @@ def test_triton_quantized_linear(hip):
                                       (96, 5121, 384, 128), (128, 5120, 640, 64),
                                       # split-K with 32-row M tiles; 64 x 64 tiles and split-K for M > 128
                                       (24, 4100, 1024, 128), (32, 1000, 512, 64), (160, 4100, 512, 128),
-                                      (200, 2000, 512, 128)])
+                                      (200, 2000, 512, 128),
+                                      # 112-row register workgroups (250 of them), ragged last one
+                                      (5, 27900, 1024, 64), (16, 27904, 512, 128)])
 def test_linear_dequant_gemm(hip, xdt, bits, M, N, K, gs):
     """M > 4: dequantise-then-MFMA kernels (split-K and tiled), ragged N and M,
     groups of 32-128 (one group per 32-code chunk), bias; through
@@ -528,7 +530,7 @@ def _c4_weights(N, K, bits):
 
 
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("M", [1, 16, 128])
+@pytest.mark.parametrize("M", [1, 3, 16, 64, 128])
 @pytest.mark.parametrize("bits", [3, 4])
 @pytest.mark.parametrize("N,K", [(4096, 4096), (14336, 4096), (4096, 14336), (28672, 4096)])
 def test_linear_config4_shapes(hip, xdt, M, bits, N, K):
