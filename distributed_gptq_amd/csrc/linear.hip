@@ -1806,6 +1806,15 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
     // 14336 x 4096 at M = 128 / 64 / 32: 46 / 30 / 27 against 51 / 42 / 41.
     const int sp = rx_splits(a, BITS);
     if (sp == 1 || (sp > 1 && a.part && static_cast<size_t>(sp) * a.M * a.N * sizeof(float) <= a.part_bytes)) {
+      // unsplit with at most 256 workgroups of 112 rows (24449-28672 rows):
+      // 7 compute waves, so that every CU has one (28672 x 4096, 4-bit M =
+      // 128 / 32: 69.4 / 38.0 against 70.4 / 39.2 us; 3-bit M = 32 37.3
+      // against 40.8; 24576 x 4096 M = 128 64.1 against 67.4)
+      if (sp == 1 && cdiv(a.N, 112) <= 256) {
+        if (a.M <= 32) return launch_rx<BITS, BF16, 16, 7, 1, 32, 4, 2>(st, a);
+        if (a.M <= 64) return launch_rx<BITS, BF16, 16, 7, 2, 64, 4, 2>(st, a);
+        return launch_rx<BITS, BF16, 16, 7, 2, 128, 4, 2>(st, a);
+      }
       if (a.M <= 32) return launch_rx<BITS, BF16, 16, 8, 1, 32, 4, 2>(st, a, sp);
       if (a.M <= 64) return launch_rx<BITS, BF16, 16, 8, 2, 64, 4, 2>(st, a, sp);
       return launch_rx<BITS, BF16, 16, 8, 2, 128, 4, 2>(st, a, sp);
