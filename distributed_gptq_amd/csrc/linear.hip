@@ -1731,20 +1731,58 @@ int launch_rx(hipStream_t st, const LinArgs& a, int splits = 1) {
   return check_launch("splitk_reduce");
 }
 
-// split-K factor of the register-decoded kernel for 16 < M <= 128: enough
-// K splits that the 128-row workgroups cover every CU (1 on layers of >= 192
-// workgroups); 0 when the layout does not take it, and for M <= 32 on layers
-// of <= 2^24 weights (measured on MI355X at 4096 x 4096, M = 24 / 32:
-// dq_split_k 12.5 / 13.6 us against 15.4 / 15.9 us)
-inline int rx_splits(const LinArgs& a, int bits) {
-  if (!((bits == 4 || bits == 3) && a.M > 16 && a.M <= 128 && (bits == 4 || a.pitch % 4 == 0))) return 0;
-  if (a.M <= 32 && a.N * a.K <= (int64_t(1) << 24)) return 0;
-  const int64_t wgs = cdiv(a.N, 128), nblk = a.K / 128;
-  if (wgs >= 192) return 1;
-  int64_t s = std::min<int64_t>(nblk, std::max<int64_t>(1, 256 / wgs));
-  s = cdiv(nblk, cdiv(nblk, s));  // no empty split
-  if (s < 2 || a.N % 4 != 0) return 0;
-  return static_cast<int>(s);
+// Plan of the register-decoded kernel for 16 < M <= 128: compute waves per
+// workgroup (8 or 7, i.e. 128 or 112 weight rows) and K splits, chosen so
+// that the workgroups fill the 256 CUs as evenly as one round allows.
+//  * >= 192 workgroups of 128 rows: unsplit, 7 waves when <= 256 workgroups
+//    of 112 rows cover the layer (24449-28672 rows), else 8.
+//  * otherwise, for each wave count, as many K splits as keep the grid
+//    within 256 workgroups (none empty), and the wave count whose grid is
+//    larger (8 on a tie); unsplit when that is one split and still >= 128
+//    workgroups.
+// splits = 0: the layout, or M <= 32 on layers of <= 2^24 weights, goes to
+// the other kernels (measured at 4096 x 4096, M = 24 / 32: dq_split_k 12.5 /
+// 13.6 us against 15.4 / 15.9 us), as does a plan of < 128 workgroups.
+// Measured on MI355X (4-bit, M = 128 / 64 / 32, us): 17408-22016 x 4096
+// unsplit on 7 waves 59-61 / 39-40 / 35-36 against 92-94 / 52 / 49-51 on the
+// tile kernels; 14336 x 4096 split in 2 on 7 waves 42.8 / 29.4 / 24.9 against
+// 45.3 / 30.4 / 26.2 on 8; 13824 x 5120 49.4 / 33.4 / 27.4 against 52.6 / 35.1
+// / 29.1.
+struct RxPlan {
+  int splits = 0;
+  int waves = 8;
+};
+
+inline RxPlan rx_plan(const LinArgs& a, int bits) {
+  RxPlan p;
+  if (!((bits == 4 || bits == 3) && a.M > 16 && a.M <= 128 && (bits == 4 || a.pitch % 4 == 0))) return p;
+  if (a.M <= 32 && a.N * a.K <= (int64_t(1) << 24)) return p;
+  const int64_t nblk = a.K / 128, cols8 = cdiv(a.N, 128), cols7 = cdiv(a.N, 112);
+  if (cols8 >= 192) {
+    p.splits = 1;
+    p.waves = cols7 <= 256 ? 7 : 8;
+    return p;
+  }
+  auto splits_for = [&](int64_t cols) {
+    int64_t sp = std::min<int64_t>(nblk, std::max<int64_t>(1, 256 / cols));
+    return cdiv(nblk, cdiv(nblk, sp));  // no empty split
+  };
+  const int64_t s8 = splits_for(cols8), s7 = splits_for(cols7);
+  const bool w7 = cols7 * s7 > cols8 * s8;
+  const int64_t sp = w7 ? s7 : s8, grid = w7 ? cols7 * s7 : cols8 * s8;
+  if ((sp > 1 && a.N % 4 != 0) || (sp == 1 && grid < 128)) return p;
+  p.splits = static_cast<int>(sp);
+  p.waves = w7 ? 7 : 8;
+  return p;
+}
+
+// the register-decoded kernel with W compute waves, activation tiles of 32,
+// 64 or 128 rows by M
+template <int BITS, bool BF16, int W>
+int launch_rx_w(hipStream_t st, const LinArgs& a, int splits) {
+  if (a.M <= 32) return launch_rx<BITS, BF16, 16, W, 1, 32, 4, 2>(st, a, splits);
+  if (a.M <= 64) return launch_rx<BITS, BF16, 16, W, 2, 64, 4, 2>(st, a, splits);
+  return launch_rx<BITS, BF16, 16, W, 2, 128, 4, 2>(st, a, splits);
 }
 
 template <int BITS, bool BF16, int NT, int MT, int WAVES>
@@ -1796,29 +1834,16 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
     }
   }
   if constexpr (BITS == 4 || BITS == 3) {
-    // 16 < M <= 128: the register-decoded kernel with activation tiles of
-    // 32, 64 or 128 rows, unsplit on wide layers (>= 192 workgroups of 128
-    // weight rows), else with K split over workgroups so that about 256 of
-    // them run when the caller's workspace holds the fp32 partial sums.
+    // 16 < M <= 128: the register-decoded kernel, split over K when the
+    // caller's workspace holds the fp32 partial sums (else the kernels below).
     // Measured on MI355X (4-bit, us; before: the tile and split kernels below):
     // 28672 x 4096 at M = 128 / 64 / 32: 69 / 45 / 40 against 98 / 56 / 53;
     // 4096 x 14336 at M = 128 / 64 / 32: 50 / 38 / 33 against 112 / 67 / 39;
-    // 14336 x 4096 at M = 128 / 64 / 32: 46 / 30 / 27 against 51 / 42 / 41.
-    const int sp = rx_splits(a, BITS);
-    if (sp == 1 || (sp > 1 && a.part && static_cast<size_t>(sp) * a.M * a.N * sizeof(float) <= a.part_bytes)) {
-      // unsplit with at most 256 workgroups of 112 rows (24449-28672 rows):
-      // 7 compute waves, so that every CU has one (28672 x 4096, 4-bit M =
-      // 128 / 32: 69.4 / 38.0 against 70.4 / 39.2 us; 3-bit M = 32 37.3
-      // against 40.8; 24576 x 4096 M = 128 64.1 against 67.4)
-      if (sp == 1 && cdiv(a.N, 112) <= 256) {
-        if (a.M <= 32) return launch_rx<BITS, BF16, 16, 7, 1, 32, 4, 2>(st, a);
-        if (a.M <= 64) return launch_rx<BITS, BF16, 16, 7, 2, 64, 4, 2>(st, a);
-        return launch_rx<BITS, BF16, 16, 7, 2, 128, 4, 2>(st, a);
-      }
-      if (a.M <= 32) return launch_rx<BITS, BF16, 16, 8, 1, 32, 4, 2>(st, a, sp);
-      if (a.M <= 64) return launch_rx<BITS, BF16, 16, 8, 2, 64, 4, 2>(st, a, sp);
-      return launch_rx<BITS, BF16, 16, 8, 2, 128, 4, 2>(st, a, sp);
-    }
+    // 14336 x 4096 at M = 128 / 64 / 32: 43 / 29 / 25 against 51 / 42 / 41.
+    const RxPlan p = rx_plan(a, BITS);
+    if (p.splits == 1 ||
+        (p.splits > 1 && a.part && static_cast<size_t>(p.splits) * a.M * a.N * sizeof(float) <= a.part_bytes))
+      return p.waves == 7 ? launch_rx_w<BITS, BF16, 7>(st, a, p.splits) : launch_rx_w<BITS, BF16, 8>(st, a, p.splits);
   }
   if (a.M <= 16) {
     if (a.N >= 64 * 256) return launch_split<BITS, BF16, 64, 16, 8>(st, a);
@@ -2078,7 +2103,7 @@ size_t splitk_bytes(int64_t M, int64_t N, int64_t K, int bits, int group_size, i
   a.K = K;
   a.pitch = (K * bits + 7) / 8;
   // M <= 16: the register path stages <= 128 groups per row
-  const int sp = M > 16 ? rx_splits(a, bits)
+  const int sp = M > 16 ? rx_plan(a, bits).splits
                         : (bits == 4 || bits == 3) && cdiv(K, group_size) <= 128 ? reg4_mid_splits(a) : 0;
   return sp > 1 ? static_cast<size_t>(sp) * M * N * sizeof(float) : 0;
 }

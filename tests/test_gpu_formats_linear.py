@@ -346,10 +346,14 @@ def _linear_plain(x, packed, bits, scales, zeros, K, gs, bias):
     # more than 256 workgroups of 112 rows: 8 compute waves of 16 rows
     (128, 28800, 256, 128, "int", torch.float16),
     (40, 32772, 384, 64, "frac", torch.float16),
-    (17, 28804, 256, 32, "int", torch.float16)])
+    (17, 28804, 256, 32, "int", torch.float16),
+    # 16385-24448 rows: unsplit on 7 waves (fewer than 192 workgroups of 128 rows)
+    (128, 20480, 256, 128, "int", torch.float16),
+    (40, 17410, 384, 64, "frac", torch.float16),
+    (20, 22018, 1024, 32, "int", torch.float32)])
 def test_linear_register_decoded_wide(hip, xdt, bits, M, N, K, gs, zkind, sdt):
-    """16 < M <= 128 on layers of >= 192 x 128 rows (7 compute waves of 16
-    rows up to 256 x 112 rows, 8 beyond): the kernel that decodes
+    """16 < M <= 128 on layers of more than 16384 rows, unsplit (7 compute
+    waves of 16 rows up to 256 x 112 rows, 8 beyond): the kernel that decodes
     the codes in registers (loader waves stage X), against the fp64 oracle."""
     from distributed_gptq_amd import _ops
     codes, scales, zeros, x = _case(M, N, K, bits, gs, M + N + bits + K, xdt)
