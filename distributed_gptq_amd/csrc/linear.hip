@@ -22,7 +22,7 @@
 //    v_mfma_f32_16x16x32_{f16,bf16} (dq_split_k: the waves of a workgroup
 //    split K over 128-column blocks and reduce through LDS; dq_tile_k:
 //    128-row weight tiles x 64/128 activation rows, double-buffered LDS).
-//  * dq_rx_k (16 < M <= 128): the codes are decoded in registers straight
+//  * dq_rx_k (16 < M <= 384): the codes are decoded in registers straight
 //    into the MFMA operands; X is staged in LDS by loader waves.  Layers of
 //    fewer than 192 x 128 rows split K over workgroups when the caller gives
 //    a workspace for the fp32 partial sums (splitk_reduce_k adds them in
@@ -1459,7 +1459,7 @@ __global__ __launch_bounds__(256) void dq_tile_k(LinArgs a) {
       }
 }
 
-// Products with 4- or 3-bit codes and 16 < M <= 128 (K % 128 == 0, group
+// Products with 4- or 3-bit codes and 16 < M <= 384 (K % 128 == 0, group
 // size % 32 == 0): the weights never pass through LDS.  A workgroup owns
 // NW * WAVES weight rows x MT activation rows over its range of K (all of K,
 // or one of gridDim.z equal ranges of 128-column blocks), with
@@ -1731,11 +1731,13 @@ int launch_rx(hipStream_t st, const LinArgs& a, int splits = 1) {
   return check_launch("splitk_reduce");
 }
 
-// Plan of the register-decoded kernel for 16 < M <= 128: compute waves per
+// Plan of the register-decoded kernel for 16 < M <= 384: compute waves per
 // workgroup (8 or 7, i.e. 128 or 112 weight rows) and K splits, chosen so
-// that the workgroups fill the 256 CUs as evenly as one round allows.
+// that the workgroups fill the 256 CUs as evenly as one round allows.  The
+// grid counts below include the activation tiles (128 rows each for M > 128).
 //  * >= 192 workgroups of 128 rows: unsplit, 7 waves when <= 256 workgroups
-//    of 112 rows cover the layer (24449-28672 rows), else 8.
+//    of 112 rows cover the layer (24449-28672 rows at M <= 128) or when the
+//    grid takes more than one round anyway, else 8.
 //  * otherwise, for each wave count, as many K splits as keep the grid
 //    within 256 workgroups (none empty), and the wave count whose grid is
 //    larger (8 on a tie); unsplit when that is one split and still >= 128
@@ -1747,7 +1749,11 @@ int launch_rx(hipStream_t st, const LinArgs& a, int splits = 1) {
 // unsplit on 7 waves 59-61 / 39-40 / 35-36 against 92-94 / 52 / 49-51 on the
 // tile kernels; 14336 x 4096 split in 2 on 7 waves 42.8 / 29.4 / 24.9 against
 // 45.3 / 30.4 / 26.2 on 8; 13824 x 5120 49.4 / 33.4 / 27.4 against 52.6 / 35.1
-// / 29.1.
+// / 29.1.  M = 192 / 256 / 320 (against the tile kernels): 4096 x 4096 31 /
+// 31 / 38 against 40 / 41 / 48; 14336 x 4096 62 / 64 / 111 against 88 / 88 /
+// 170; 4096 x 14336 71 / 73 / 110 against 129 / 129 / 156; 28672 x 4096 123
+// / 128 / 176 against 174 / 178 / 257; 5120 x 13824 82 / 85 / 113 against
+// 125 / 151 / 156.
 struct RxPlan {
   int splits = 0;
   int waves = 8;
@@ -1755,12 +1761,13 @@ struct RxPlan {
 
 inline RxPlan rx_plan(const LinArgs& a, int bits) {
   RxPlan p;
-  if (!((bits == 4 || bits == 3) && a.M > 16 && a.M <= 128 && (bits == 4 || a.pitch % 4 == 0))) return p;
+  if (!((bits == 4 || bits == 3) && a.M > 16 && a.M <= 384 && (bits == 4 || a.pitch % 4 == 0))) return p;
   if (a.M <= 32 && a.N * a.K <= (int64_t(1) << 24)) return p;
-  const int64_t nblk = a.K / 128, cols8 = cdiv(a.N, 128), cols7 = cdiv(a.N, 112);
+  const int64_t mt = cdiv(a.M, 128);
+  const int64_t nblk = a.K / 128, cols8 = cdiv(a.N, 128) * mt, cols7 = cdiv(a.N, 112) * mt;
   if (cols8 >= 192) {
     p.splits = 1;
-    p.waves = cols7 <= 256 ? 7 : 8;
+    p.waves = cols7 <= 256 || cols8 > 256 ? 7 : 8;
     return p;
   }
   auto splits_for = [&](int64_t cols) {
@@ -1777,7 +1784,7 @@ inline RxPlan rx_plan(const LinArgs& a, int bits) {
 }
 
 // the register-decoded kernel with W compute waves, activation tiles of 32,
-// 64 or 128 rows by M
+// 64 or 128 rows by M (M > 128: several tiles of 128)
 template <int BITS, bool BF16, int W>
 int launch_rx_w(hipStream_t st, const LinArgs& a, int splits) {
   if (a.M <= 32) return launch_rx<BITS, BF16, 16, W, 1, 32, 4, 2>(st, a, splits);
@@ -1795,7 +1802,7 @@ int launch_split(hipStream_t st, const LinArgs& a) {
 
 // M <= 16: the register path (4/3-bit) or split-K with 16 waves, weight rows
 // per workgroup chosen so that the grid stays >= 256 workgroups while X is
-// re-read by fewer of them.  16 < M <= 128 with 4/3-bit codes: the
+// re-read by fewer of them.  16 < M <= 384 with 4/3-bit codes: the
 // register-decoded kernel where its layout and workspace allow.  Otherwise,
 // M > 16 (measured on MI355X at N x K = 28672 x
 // 4096, 14336 x 4096, 4096 x 14336 and 4096 x 4096, M = 32-128): 64 x 64
@@ -1834,7 +1841,7 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
     }
   }
   if constexpr (BITS == 4 || BITS == 3) {
-    // 16 < M <= 128: the register-decoded kernel, split over K when the
+    // 16 < M <= 384: the register-decoded kernel, split over K when the
     // caller's workspace holds the fp32 partial sums (else the kernels below).
     // Measured on MI355X (4-bit, us; before: the tile and split kernels below):
     // 28672 x 4096 at M = 128 / 64 / 32: 69 / 45 / 40 against 98 / 56 / 53;

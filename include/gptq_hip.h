@@ -229,10 +229,11 @@ int gptq_linear(const void* x, int x_dtype, int64_t M, const uint8_t* packed,
 
 /* gptq_linear with a caller workspace (perm may be NULL): with perm, x is
  * gathered through it into the workspace first (as gptq_linear_perm); the
- * rest of the workspace lets the M = 65..128 kernel split K over more
- * workgroups on narrower layers, its fp32 partial sums reduced in split
- * order (deterministic).  gptq_linear_workspace_size gives the bytes for
- * both (has_perm: 0 or 1); with less, the layer runs as gptq_linear would.
+ * rest of the workspace (from its first 256-byte boundary) lets the kernels
+ * for 1 < M <= 384 split K over more workgroups on narrower layers, their
+ * fp32 partial sums reduced in split order (deterministic).
+ * gptq_linear_workspace_size gives the bytes for both (has_perm: 0 or 1);
+ * with less, the layer runs as gptq_linear would.
  * Same semantics as gptq_linear; no counterpart in the reference beyond
  * torch.ops.gptq.linear (models/layers.py:151-157). */
 size_t gptq_linear_workspace_size(int64_t M, int64_t N, int64_t K, int bits,

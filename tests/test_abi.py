@@ -68,6 +68,10 @@ def test_library_loads_and_reports_version():
     assert h.gptq_linear_workspace_size(17, 4096, 14336, 3, 128, bf16, 0) == 8 * 17 * 4096 * 4
     assert h.gptq_linear_workspace_size(32, 4096, 4096, 4, 128, bf16, 0) == 0     # M <= 32 on 2^24 weights
     assert h.gptq_linear_workspace_size(16, 4096, 14336, 4, 128, bf16, 0) == 0    # M <= 16 at 4096 rows
+    # M > 128: the grid counts two activation tiles (4096 rows: 4 splits)
+    assert h.gptq_linear_workspace_size(256, 4096, 4096, 4, 128, bf16, 0) == 4 * 256 * 4096 * 4
+    assert h.gptq_linear_workspace_size(256, 28672, 4096, 4, 128, bf16, 0) == 0
+    assert h.gptq_linear_workspace_size(400, 4096, 4096, 4, 128, bf16, 0) == 0    # M > 384
     # 1 < M <= 16 on 4097-8191 rows with K >= 8192: K in 3 ranges
     assert h.gptq_linear_workspace_size(16, 5120, 13824, 4, 128, bf16, 0) == 3 * 16 * 5120 * 4
     assert h.gptq_linear_workspace_size(5, 5120, 13824, 3, 128, bf16, 0) == 3 * 5 * 5120 * 4

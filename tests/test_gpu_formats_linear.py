@@ -347,6 +347,9 @@ def _linear_plain(x, packed, bits, scales, zeros, K, gs, bias):
     (128, 28800, 256, 128, "int", torch.float16),
     (40, 32772, 384, 64, "frac", torch.float16),
     (17, 28804, 256, 32, "int", torch.float16),
+    # two activation tiles: more than 256 workgroups, 7 waves
+    (192, 24576, 256, 128, "int", torch.float16),
+    (300, 16448, 384, 64, "frac", torch.float16),
     # 16385-24448 rows: unsplit on 7 waves (fewer than 192 workgroups of 128 rows)
     (128, 20480, 256, 128, "int", torch.float16),
     (40, 17410, 384, 64, "frac", torch.float16),
@@ -386,9 +389,13 @@ def test_linear_register_decoded_wide(hip, xdt, bits, M, N, K, gs, zkind, sdt):
     (64, 4096, 1024, 128, "int", torch.float16, False),
     (50, 5120, 1408, 64, "frac", torch.float16, True),
     (32, 2048, 8320, 128, "int", torch.float32, False),
-    (17, 1028, 17408, 32, "int", torch.float16, True)])
+    (17, 1028, 17408, 32, "int", torch.float16, True),
+    # M > 128: two or three 128-row activation tiles per workgroup column
+    (256, 4096, 1024, 128, "int", torch.float16, False),
+    (384, 4096, 512, 64, "frac", torch.float16, True),
+    (150, 2052, 1024, 32, "int", torch.float32, False)])
 def test_linear_register_decoded_split_k(hip, xdt, bits, M, N, K, gs, zkind, sdt, act):
-    """16 < M <= 128 on layers of < 192 x 128 rows: the register-decoded
+    """16 < M <= 384 on layers too narrow to fill the GPU unsplit: the register-decoded
     kernel with K split over workgroups (fp32 partials in the workspace,
     reduced in split order, bias added there), against the fp64 oracle;
     the same call twice gives identical bits."""
