@@ -600,6 +600,26 @@ def test_linear_perm_matches_oracle(hip, xdt, bits, M, N, K):
     assert err < TOL[xdt], err
 
 
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bits,gs", [(4, 128), (3, 128), (8, 64), (2, 32)])
+@pytest.mark.parametrize("N,K", [(1000, 4096), (300, 14336), (4100, 1024), (64, 32768)])
+def test_linear_perm_m1_equals_pregathered_x(hip, xdt, bits, gs, N, K):
+    """M = 1 with perm (x gathered through perm, then the GEMV): the result
+    equals, bit for bit, the GEMV on x gathered beforehand, and the oracle
+    within the fast path's tolerance."""
+    from distributed_gptq_amd import _ops
+    codes, scales, zeros, x = _case(1, N, K, bits, gs, N + K + bits, xdt)
+    perm = np.random.default_rng(K + bits).permutation(K).astype(np.int32)
+    packed = torch.from_numpy(O.pack_bitstream(codes, bits)).cuda()
+    xc, sc, zc, pc = x.cuda(), scales.cuda(), zeros.cuda(), torch.from_numpy(perm).cuda()
+    y = _ops.linear(xc, packed, bits, sc, zc, K, group_size=gs, perm=pc)
+    y_pre = _ops.linear(xc[:, pc.long()].contiguous(), packed, bits, sc, zc, K, group_size=gs)
+    assert torch.equal(y, y_pre)
+    ref = O.linear(x.float().numpy()[:, perm], codes, scales.numpy(), zeros.numpy(), np.arange(K) // gs)
+    err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err < TOL[xdt], err
+
+
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("K,gs", [(200, 50), (204, 51), (1003, 59)])
 def test_linear_perm_generic_and_fp32(hip, xdt, K, gs):
