@@ -1,0 +1,66 @@
+"""gptq::linear captured in a HIP graph: every route (the M = 1 GEMV, the act-order
+gather, the register kernels with and without split-K partial sums in the
+workspace, several activation tiles) replays to the eager result bit for bit,
+replay after replay, with eager work and synchronisations in between, and reads
+x at replay time."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gptq_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(M, N, K, bits, gs, act, seed):
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(0, 2 ** bits, (N, K)).astype(np.uint8)
+    scales = torch.from_numpy(rng.uniform(1e-3, 1e-2, (N, K // gs))).half().cuda()
+    zeros = torch.from_numpy(rng.integers(0, 2 ** bits, (N, K // gs)).astype(np.float64)).half().cuda()
+    packed = torch.from_numpy(O.pack_bitstream(codes, bits)).cuda()
+    perm = torch.from_numpy(rng.permutation(K).astype(np.int32)).cuda() if act else None
+    bias = torch.from_numpy(rng.standard_normal(N)).half().cuda()
+    xs = [torch.from_numpy(rng.standard_normal((M, K))).half().cuda() for _ in range(3)]
+    return packed, scales, zeros, perm, bias, xs
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs,act", [
+    (1, 4096, 4096, 4, 128, False),      # GEMV
+    (1, 4096, 4096, 4, 128, True),       # gather into the workspace, then the GEMV
+    (16, 5120, 8192, 4, 128, False),     # 32-row register workgroups, K in 3 ranges, reduce
+    (128, 4096, 4096, 3, 128, False),    # register-decoded, 8 K ranges, reduce
+    (64, 24576, 512, 4, 64, False),      # register-decoded unsplit on 7 waves
+    (256, 4096, 1024, 4, 128, True),     # gather + two activation tiles + split-K
+])
+def test_linear_graph_replays_match_eager(hip, M, N, K, bits, gs, act):
+    from distributed_gptq_amd import _ops
+    packed, scales, zeros, perm, bias, xs = _inputs(M, N, K, bits, gs, act, M + N + K)
+
+    def op(x, out=None):
+        return _ops.linear(x, packed, bits, scales, zeros, K, group_size=gs, bias=bias, perm=perm, out=out)
+
+    eager = [op(x) for x in xs]
+    torch.cuda.synchronize()
+    x_in = xs[0].clone()
+    y = torch.empty(M, N, dtype=torch.float16, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        op(x_in, out=y)  # the stream's workspace is allocated outside the capture
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            op(x_in, out=y)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for r in range(6):
+        i = r % 3
+        x_in.copy_(xs[i])
+        y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        # eager work of the program's own between replays
+        other = op(xs[(i + 1) % 3])
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager[i]), (r, i)
+        assert torch.equal(other, eager[(i + 1) % 3]), r
