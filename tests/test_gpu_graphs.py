@@ -64,3 +64,39 @@ def test_linear_graph_replays_match_eager(hip, M, N, K, bits, gs, act):
         torch.cuda.synchronize()
         assert torch.equal(y, eager[i]), (r, i)
         assert torch.equal(other, eager[(i + 1) % 3]), r
+
+
+@pytest.mark.parametrize("n,K,dt", [(4096, 768, torch.bfloat16), (3000, 1000, torch.float16),
+                                    (32768, 3072, torch.bfloat16)])
+def test_hessian_graph_replays_accumulate_like_eager(hip, n, K, dt):
+    """H += X^T X captured in a HIP graph: each replay adds exactly what the
+    same eager call adds (token splits, partial tiles in the workspace and
+    their reduce included), with eager work between the replays."""
+    from distributed_gptq_amd import _ops
+    g = torch.Generator(device="cuda").manual_seed(n + K)
+    X = torch.randn(n, K, generator=g, device="cuda").to(dt)
+    X2 = torch.randn(n // 2, K, generator=g, device="cuda").to(dt)
+    He = torch.zeros(K, K, device="cuda")
+    snaps = []
+    for _ in range(3):
+        _ops.hessian_accumulate(He, X)
+        snaps.append(He.clone())
+    Hg = torch.zeros(K, K, device="cuda")
+    Hw = torch.zeros(K, K, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        _ops.hessian_accumulate(Hw, X)  # the stream's workspace is allocated outside the capture
+        s.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            _ops.hessian_accumulate(Hg, X)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    Hg.zero_()
+    other = torch.zeros(K, K, device="cuda")
+    for r in range(3):
+        graph.replay()
+        _ops.hessian_accumulate(other, X2)  # eager work between the replays
+        torch.cuda.synchronize()
+        assert torch.equal(Hg, snaps[r]), r
