@@ -393,7 +393,10 @@ def test_linear_register_decoded_wide(hip, xdt, bits, M, N, K, gs, zkind, sdt):
     # M > 128: two or three 128-row activation tiles per workgroup column
     (256, 4096, 1024, 128, "int", torch.float16, False),
     (384, 4096, 512, 64, "frac", torch.float16, True),
-    (150, 2052, 1024, 32, "int", torch.float32, False)])
+    (150, 2052, 1024, 32, "int", torch.float32, False),
+    # a few output rows: one workgroup column, most of its weight rows past N
+    (100, 8, 1024, 128, "int", torch.float16, False),
+    (65, 4, 2048, 64, "int", torch.float16, True)])
 def test_linear_register_decoded_split_k(hip, xdt, bits, M, N, K, gs, zkind, sdt, act):
     """16 < M <= 384 on layers too narrow to fill the GPU unsplit: the register-decoded
     kernel with K split over workgroups (fp32 partials in the workspace,
