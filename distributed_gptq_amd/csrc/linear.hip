@@ -1757,29 +1757,47 @@ int launch_rx(hipStream_t st, const LinArgs& a, int splits = 1) {
 struct RxPlan {
   int splits = 0;
   int waves = 8;
+  int rows = 16;  // weight rows per compute wave
 };
 
-inline RxPlan rx_plan(const LinArgs& a, int bits) {
+inline RxPlan rx_plan(const LinArgs& a, int bits, bool rows32 = true) {
   RxPlan p;
   if (!((bits == 4 || bits == 3) && a.M > 16 && a.M <= 384 && (bits == 4 || a.pitch % 4 == 0))) return p;
   if (a.M <= 32 && a.N * a.K <= (int64_t(1) << 24)) return p;
   const int64_t mt = cdiv(a.M, 128);
   const int64_t nblk = a.K / 128, cols8 = cdiv(a.N, 128) * mt, cols7 = cdiv(a.N, 112) * mt;
-  if (cols8 >= 192) {
-    p.splits = 1;
-    p.waves = cols7 <= 256 || cols8 > 256 ? 7 : 8;
-    return p;
-  }
   auto splits_for = [&](int64_t cols) {
     int64_t sp = std::min<int64_t>(nblk, std::max<int64_t>(1, 256 / cols));
     return cdiv(nblk, cdiv(nblk, sp));  // no empty split
   };
-  const int64_t s8 = splits_for(cols8), s7 = splits_for(cols7);
-  const bool w7 = cols7 * s7 > cols8 * s8;
-  const int64_t sp = w7 ? s7 : s8, grid = w7 ? cols7 * s7 : cols8 * s8;
-  if ((sp > 1 && a.N % 4 != 0) || (sp == 1 && grid < 128)) return p;
-  p.splits = static_cast<int>(sp);
-  p.waves = w7 ? 7 : 8;
+  int64_t grid = 0;
+  if (cols8 >= 192) {
+    p.splits = 1;
+    p.waves = cols7 <= 256 || cols8 > 256 ? 7 : 8;
+    grid = p.waves == 7 ? cols7 : cols8;
+  } else {
+    const int64_t s8 = splits_for(cols8), s7 = splits_for(cols7);
+    const bool w7 = cols7 * s7 > cols8 * s8;
+    const int64_t sp = w7 ? s7 : s8;
+    grid = w7 ? cols7 * s7 : cols8 * s8;
+    if ((sp > 1 && a.N % 4 != 0) || (sp == 1 && grid < 128)) return p;
+    p.splits = static_cast<int>(sp);
+    p.waves = w7 ? 7 : 8;
+  }
+  // 64 < M <= 128: 32 rows per compute wave (7 compute waves, 224 rows per
+  // workgroup) read each X fragment for two row blocks, where its grid is at
+  // least as large with at most 8 splits (measured, 4-bit M = 128, us: 28672 x
+  // 4096 68.3 -> 66.2, 14336 x 4096 44.0 -> 41.9, 13824 x 5120 50.1 -> 46.2,
+  // 22016 x 4096 63.2 -> 59.1, 11008 x 4096 40.7 -> 38.8; where its grid is
+  // smaller, slower: 16384 x 4096 47.5 -> 48.7, 8192 x 8192 49.6 -> 52.7)
+  if (rows32 && a.M > 64 && a.M <= 128) {
+    const int64_t cols32 = cdiv(a.N, 224), s32 = splits_for(cols32);
+    if (s32 <= 8 && cols32 * s32 >= grid && (s32 == 1 || a.N % 4 == 0)) {
+      p.splits = static_cast<int>(s32);
+      p.waves = 7;
+      p.rows = 32;
+    }
+  }
   return p;
 }
 
@@ -1847,10 +1865,18 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
     // 28672 x 4096 at M = 128 / 64 / 32: 69 / 45 / 40 against 98 / 56 / 53;
     // 4096 x 14336 at M = 128 / 64 / 32: 50 / 38 / 33 against 112 / 67 / 39;
     // 14336 x 4096 at M = 128 / 64 / 32: 43 / 29 / 25 against 51 / 42 / 41.
-    const RxPlan p = rx_plan(a, BITS);
-    if (p.splits == 1 ||
-        (p.splits > 1 && a.part && static_cast<size_t>(p.splits) * a.M * a.N * sizeof(float) <= a.part_bytes))
+    auto fits = [&](const RxPlan& q) {
+      return q.splits == 1 ||
+             (q.splits > 1 && a.part && static_cast<size_t>(q.splits) * a.M * a.N * sizeof(float) <= a.part_bytes);
+    };
+    RxPlan p = rx_plan(a, BITS);
+    if (p.rows == 32 && !fits(p)) p = rx_plan(a, BITS, false);  // no room for its partial sums
+    if (fits(p)) {
+      // 32 rows per wave: 8 waves in all (one loader), so that each has 256
+      // registers (with 10 waves it spilled), and two code slots
+      if (p.rows == 32) return launch_rx<BITS, BF16, 32, 7, 1, 128, 2, 2>(st, a, p.splits);
       return p.waves == 7 ? launch_rx_w<BITS, BF16, 7>(st, a, p.splits) : launch_rx_w<BITS, BF16, 8>(st, a, p.splits);
+    }
   }
   if (a.M <= 16) {
     if (a.N >= 64 * 256) return launch_split<BITS, BF16, 64, 16, 8>(st, a);

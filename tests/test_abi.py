@@ -63,7 +63,9 @@ def test_library_loads_and_reports_version():
         (100 * 4096 * 2 + 255) // 256 * 256 + 8 * 100 * 4096 * 4
     # 11 blocks of 128 over 6 splits at 5120 rows (40 workgroups)
     assert h.gptq_linear_workspace_size(128, 5120, 1408, 3, 64, bf16, 0) == 6 * 128 * 5120 * 4
-    assert h.gptq_linear_workspace_size(128, 28672, 4096, 4, 128, bf16, 0) == 0   # 224 workgroups
+    # 64 < M <= 128 at 28672 rows: 128 workgroups of 224 rows, K in 2 ranges
+    assert h.gptq_linear_workspace_size(128, 28672, 4096, 4, 128, bf16, 0) == 2 * 128 * 28672 * 4
+    assert h.gptq_linear_workspace_size(64, 28672, 4096, 4, 128, bf16, 0) == 0    # unsplit, 7 waves
     assert h.gptq_linear_workspace_size(64, 4096, 14336, 4, 128, bf16, 0) == 8 * 64 * 4096 * 4
     assert h.gptq_linear_workspace_size(17, 4096, 14336, 3, 128, bf16, 0) == 8 * 17 * 4096 * 4
     assert h.gptq_linear_workspace_size(32, 4096, 4096, 4, 128, bf16, 0) == 0     # M <= 32 on 2^24 weights
