@@ -1293,6 +1293,14 @@ inline int reg4_mid_splits(const LinArgs& a) {
   return a.K >= 8192 && 3 * cdiv(a.N, 32) <= 512 && a.N % 4 == 0 ? 3 : 1;
 }
 
+// 1 < M <= 16 on 8192-row layers: 128 workgroups of 64 rows, so K split in
+// 2 (measured on MI355X, 4-bit 8192 x 8192, M = 16 / 4: 21.5 / 19.2 us
+// against 26.0 / 22.2 unsplit; on 11008-14336 rows, where the unsplit grid
+// is 172-224 workgroups, splitting measured 15-40% slower).  0 elsewhere.
+inline int reg4_wide_splits(const LinArgs& a) {
+  return a.M > 1 && a.M <= 16 && a.N >= 8192 && cdiv(a.N, 64) * 2 <= 256 && a.N % 4 == 0 && a.K >= 256 ? 2 : 0;
+}
+
 // Large products (M > 16 and enough output tiles): one workgroup per NT x MT
 // tile of (weight rows x activation rows), NT = 128 (K in steps of 64) or 64
 // (steps of 128) so that the grid fills the GPU.  Each thread loads one
@@ -1849,7 +1857,11 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
         if (w112 > 240 && w112 <= 256 && a.ngroups <= 64) return launch_reg4<BITS, 112, 8, BF16>(st, a);
         return launch_reg4<BITS, 64, 4, BF16>(st, a);
       }
-      if (a.N >= 32 * 256) return launch_reg4<BITS, 64, 8, BF16>(st, a);
+      if (a.N >= 32 * 256) {
+        const int s = reg4_wide_splits(a);
+        const bool fits = s > 1 && a.part && static_cast<size_t>(s) * a.M * a.N * sizeof(float) <= a.part_bytes;
+        return launch_reg4<BITS, 64, 8, BF16>(st, a, fits ? s : 1);
+      }
       if (const int s = reg4_mid_splits(a)) {
         const bool fits = a.part && static_cast<size_t>(s) * a.M * a.N * sizeof(float) <= a.part_bytes;
         return launch_reg4<BITS, 32, 8, BF16>(st, a, s > 1 && fits ? s : 1);
@@ -2137,7 +2149,9 @@ size_t splitk_bytes(int64_t M, int64_t N, int64_t K, int bits, int group_size, i
   a.pitch = (K * bits + 7) / 8;
   // M <= 16: the register path stages <= 128 groups per row
   const int sp = M > 16 ? rx_plan(a, bits).splits
-                        : (bits == 4 || bits == 3) && cdiv(K, group_size) <= 128 ? reg4_mid_splits(a) : 0;
+                        : (bits == 4 || bits == 3) && cdiv(K, group_size) <= 128
+                              ? std::max(reg4_mid_splits(a), reg4_wide_splits(a))
+                              : 0;
   return sp > 1 ? static_cast<size_t>(sp) * M * N * sizeof(float) : 0;
 }
 

@@ -81,6 +81,9 @@ def test_library_loads_and_reports_version():
     assert h.gptq_linear_workspace_size(16, 5120, 5120, 4, 128, bf16, 0) == 0     # K < 8192
     assert h.gptq_linear_workspace_size(2, 5120, 13824, 4, 128, bf16, 0) == 3 * 2 * 5120 * 4
     assert h.gptq_linear_workspace_size(1, 5120, 13824, 4, 128, bf16, 0) == 0     # M = 1: the GEMV
+    # 1 < M <= 16 at 8192 rows: 128 workgroups of 64 rows, K in 2 ranges
+    assert h.gptq_linear_workspace_size(16, 8192, 8192, 4, 128, bf16, 0) == 2 * 16 * 8192 * 4
+    assert h.gptq_linear_workspace_size(16, 14336, 4096, 4, 128, bf16, 0) == 0
     assert h.gptq_linear_workspace_size(16, 5122, 13824, 4, 128, bf16, 0) == 0    # N % 4
     assert h.gptq_linear_workspace_size(128, 4098, 4096, 4, 128, bf16, 0) == 0    # N % 4
     assert h.gptq_linear_workspace_size(128, 4096, 4096, 8, 128, bf16, 0) == 0    # 8-bit

@@ -431,16 +431,19 @@ def test_linear_register_decoded_split_k(hip, xdt, bits, M, N, K, gs, zkind, sdt
     (5, 5000, 8192, 64),      # ragged last workgroup, groups of 64 (per-weight dequantisation)
     (9, 6144, 4096, 128),     # unsplit (K < 8192)
     (12, 5122, 8320, 128),    # N % 4 != 0: unsplit
-    (2, 5120, 8192, 128), (3, 6148, 4096, 64)])
+    (2, 5120, 8192, 128), (3, 6148, 4096, 64),
+    # 8192 rows: 64-row workgroups, K in 2 ranges
+    (16, 8192, 1024, 128), (4, 8192, 640, 64)])
 def test_linear_register_mid_rows(hip, xdt, bits, M, N, K, gs):
     """1 < M <= 16 on layers of 4097-8191 rows: dq_reg4_k with 32-row
     workgroups, split over K (partials reduced in order, bias added there)
-    when K >= 8192 and the workspace holds the partials; through
+    when K >= 8192 and the workspace holds the partials; on 8192 rows
+    64-row workgroups with K split in 2; through
     gptq_linear_ws and, unsplit, through gptq_linear; against the fp64
     oracle."""
     from distributed_gptq_amd import _lib, _ops
     nb = _lib.lib().gptq_linear_workspace_size(M, N, K, bits, gs, _ops.dtype_code(xdt), 0)
-    assert nb == (3 * M * N * 4 if K >= 8192 and N % 4 == 0 else 0)
+    assert nb == (2 * M * N * 4 if N == 8192 else 3 * M * N * 4 if K >= 8192 and N % 4 == 0 else 0)
     codes, scales, zeros, x = _case(M, N, K, bits, gs, M + N + K + bits, xdt)
     bias = torch.randn(N).to(xdt)
     packed = torch.from_numpy(O.pack_bitstream(codes, bits)).cuda()
