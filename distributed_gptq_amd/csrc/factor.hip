@@ -367,13 +367,14 @@ int chol_inv(Ctx& c, int64_t n0, int64_t m, float* tmp) {
   // L21 = A21 X11^T   (opB = X11^T is upper: k <= j)
   rc = launch_gemm_f32(c.st, m2, m1, m1, 1.0f, A21, ld, false, X11, ld, true, 0.0f, L21, m1, GEMM_KLIM_B_LE_J);
   if (rc) return rc;
-  // S = A22 - L21 L21^T (lower triangle)
-  rc = launch_gemm_f32(c.st, m2, m2, m1, -1.0f, L21, m1, false, L21, m1, true, 1.0f, A22, ld, GEMM_C_LOWER);
+  // S = A22 - L21 L21^T (lower triangle) and T2 = L21 X11 (opB = X11 lower:
+  // k >= j): both need only L21, so they share one grid where their tiles
+  // alone would leave CUs idle (T2 is kept until X21, below the recursion)
+  const GemmCall S{m2, m2, m1, -1.0f, L21, m1, false, L21, m1, true, 1.0f, A22, ld, GEMM_C_LOWER};
+  const GemmCall LX{m2, m1, m1, 1.0f, L21, m1, false, X11, ld, false, 0.0f, T2, m1, GEMM_KLIM_B_GE_J};
+  rc = launch_gemm_f32_pair(c.st, S, LX);
   if (rc) return rc;
   rc = chol_inv(c, n0 + m1, m2, deeper);
-  if (rc) return rc;
-  // T2 = L21 X11   (opB = X11 lower: k >= j)
-  rc = launch_gemm_f32(c.st, m2, m1, m1, 1.0f, L21, m1, false, X11, ld, false, 0.0f, T2, m1, GEMM_KLIM_B_GE_J);
   if (rc) return rc;
   // X21 = -X22 T2  (opA = X22 lower: k <= i)
   return launch_gemm_f32(c.st, m2, m1, m2, -1.0f, X22, ld, false, T2, m1, false, 0.0f, X21, ld, GEMM_KLIM_A_LE_I);

@@ -127,18 +127,32 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int o
   }
 }
 
+// one product, its tile grid and dispatch order
+struct GemmDesc {
+  int64_t M, N, Kd;
+  float alpha;
+  Operand a, b;
+  float beta;
+  float* C;
+  int64_t ldc;
+  int flags, tiles_m, tiles_n, order;
+};
+
+// output tile `bid` (in dispatch order) of the product d, staged through sA / sB
 template <int TM, int TN, int BK, bool kVec, bool kTA, bool kTB>
-__global__ __launch_bounds__(kThreads) void gemm_f32_kernel(int64_t M, int64_t N, int64_t Kd, float alpha,
-                                                           Operand a, Operand b, float beta, float* __restrict__ C,
-                                                           int64_t ldc, int flags, int tiles_m, int tiles_n,
-                                                           int order) {
+__device__ __forceinline__ void gemm_tile(const GemmDesc& d, int bid, float* __restrict__ sA,
+                                          float* __restrict__ sB) {
   constexpr int P = BK + 2;
   constexpr int FM = TM / 64, FN = TN / 64;  // 32x32 blocks per wave
   constexpr int QA = TM * BK / 4 / kThreads, QB = TN * BK / 4 / kThreads;
-  __shared__ float sA[TM * P];
-  __shared__ float sB[TN * P];
+  const int64_t M = d.M, N = d.N, Kd = d.Kd, ldc = d.ldc;
+  const float alpha = d.alpha, beta = d.beta;
+  const Operand& a = d.a;
+  const Operand& b = d.b;
+  float* __restrict__ C = d.C;
+  const int flags = d.flags;
   int tm = 0, tn = 0;
-  tile_of<TM, TN>(static_cast<int>(blockIdx.x), tiles_m, tiles_n, order, tm, tn);
+  tile_of<TM, TN>(bid, d.tiles_m, d.tiles_n, d.order, tm, tn);
   const int64_t i0 = static_cast<int64_t>(tm) * TM;
   const int64_t j0 = static_cast<int64_t>(tn) * TN;
   if ((flags & GEMM_C_LOWER) && j0 > i0 + TM - 1) return;
@@ -228,6 +242,24 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(int64_t M, int64_t N
     }
 }
 
+template <int TM, int TN, int BK, bool kVec, bool kTA, bool kTB>
+__global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmDesc d) {
+  __shared__ float sA[TM * (BK + 2)];
+  __shared__ float sB[TN * (BK + 2)];
+  gemm_tile<TM, TN, BK, kVec, kTA, kTB>(d, static_cast<int>(blockIdx.x), sA, sB);
+}
+
+// two independent products in one grid (16-byte operands, opA not
+// transposed): workgroups [0, split) take tiles of d0, the rest tiles of d1
+template <int TM, int TN, int BK, bool kTB0, bool kTB1>
+__global__ __launch_bounds__(kThreads) void gemm_f32_pair_kernel(GemmDesc d0, GemmDesc d1, int split) {
+  __shared__ float sA[TM * (BK + 2)];
+  __shared__ float sB[TN * (BK + 2)];
+  const int bid = static_cast<int>(blockIdx.x);
+  if (bid < split) gemm_tile<TM, TN, BK, true, false, kTB0>(d0, bid, sA, sB);
+  else gemm_tile<TM, TN, BK, true, false, kTB1>(d1, bid - split, sA, sB);
+}
+
 struct GemmArgs {
   int64_t M, N, Kd;
   float alpha;
@@ -238,8 +270,10 @@ struct GemmArgs {
   int flags;
 };
 
-template <int TM, int TN, bool V, bool TA, bool TB>
-void launch_one(hipStream_t st, const GemmArgs& g) {
+// the tile grid of g in TM x TN tiles and its dispatch order; returns the
+// number of workgroups
+template <int TM, int TN>
+int64_t describe(const GemmArgs& g, GemmDesc& d) {
   const int tiles_m = static_cast<int>(cdiv(g.M, TM));
   const int tiles_n = static_cast<int>(cdiv(g.N, TN));
   int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
@@ -257,9 +291,16 @@ void launch_one(hipStream_t st, const GemmArgs& g) {
       break;
     default: break;
   }
-  const dim3 grid(static_cast<unsigned>(tiles));
-  hipLaunchKernelGGL((gemm_f32_kernel<TM, TN, 32, V, TA, TB>), grid, dim3(kThreads), 0, st, g.M, g.N, g.Kd, g.alpha,
-                     g.a, g.b, g.beta, g.C, g.ldc, g.flags, tiles_m, tiles_n, order);
+  d = GemmDesc{g.M, g.N, g.Kd, g.alpha, g.a, g.b, g.beta, g.C, g.ldc, g.flags, tiles_m, tiles_n, order};
+  return tiles;
+}
+
+template <int TM, int TN, bool V, bool TA, bool TB>
+void launch_one(hipStream_t st, const GemmArgs& g) {
+  GemmDesc d;
+  const int64_t tiles = describe<TM, TN>(g, d);
+  hipLaunchKernelGGL((gemm_f32_kernel<TM, TN, 32, V, TA, TB>), dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0,
+                     st, d);
 }
 
 // transposition and vector width are compile-time in the kernel
@@ -283,20 +324,54 @@ inline bool vec_ok(const Operand& o, int64_t Kd) {
   return o.ld % 4 == 0 && (reinterpret_cast<uintptr_t>(o.p) % 16) == 0 && (o.trans ? o.rows : Kd) % 4 == 0;
 }
 
+GemmArgs make_args(const GemmCall& c) {
+  return GemmArgs{c.M, c.N, c.Kd, c.alpha, Operand{c.A, c.lda, c.transA, c.M},
+                  Operand{c.B, c.ldb, !c.transB, c.N},  // B viewed as [j][k]
+                  c.beta, c.C, c.ldc, c.flags};
+}
+
+// 64 x 64 tiles below 4096 tiles of 128 x 64 (measured on MI355X: the four
+// triangular products at 3584^3 1.96 -> 1.76 ms, at 1792^3 0.42 -> 0.34 ms;
+// at 7168^3 128 x 64 stays faster, 12.8 against 13.3 ms)
+inline bool small_tiles(const GemmArgs& g) { return cdiv(g.M, 128) * cdiv(g.N, 64) < 4096; }
+
+int launch_args(hipStream_t st, const GemmArgs& g) {
+  if (g.M <= 0 || g.N <= 0) return GPTQ_OK;
+  const bool vec = vec_ok(g.a, g.Kd) && vec_ok(g.b, g.Kd);
+  if (small_tiles(g)) return launch_tiles<64, 64>(st, g, vec);
+  return launch_tiles<128, 64>(st, g, vec);
+}
+
+template <bool TB0, bool TB1>
+void launch_pair(hipStream_t st, const GemmDesc& d0, int64_t t0, const GemmDesc& d1, int64_t t1) {
+  hipLaunchKernelGGL((gemm_f32_pair_kernel<64, 64, 32, TB0, TB1>), dim3(static_cast<unsigned>(t0 + t1)),
+                     dim3(kThreads), 0, st, d0, d1, static_cast<int>(t0));
+}
+
 }  // namespace
 
 int launch_gemm_f32(hipStream_t st, int64_t M, int64_t N, int64_t Kd, float alpha, const float* A, int64_t lda,
                     bool transA, const float* B, int64_t ldb, bool transB, float beta, float* C, int64_t ldc,
                     int flags) {
-  if (M <= 0 || N <= 0) return GPTQ_OK;
-  const GemmArgs g{M, N, Kd, alpha, Operand{A, lda, transA, M}, Operand{B, ldb, !transB, N},  // B viewed as [j][k]
-                   beta, C, ldc, flags};
-  const bool vec = vec_ok(g.a, Kd) && vec_ok(g.b, Kd);
-  // 64 x 64 tiles below 4096 tiles of 128 x 64 (measured on MI355X: the four
-  // triangular products at 3584^3 1.96 -> 1.76 ms, at 1792^3 0.42 -> 0.34 ms;
-  // at 7168^3 128 x 64 stays faster, 12.8 against 13.3 ms)
-  if (cdiv(M, 128) * cdiv(N, 64) < 4096) return launch_tiles<64, 64>(st, g, vec);
-  return launch_tiles<128, 64>(st, g, vec);
+  return launch_args(st, make_args(GemmCall{M, N, Kd, alpha, A, lda, transA, B, ldb, transB, beta, C, ldc, flags}));
+}
+
+int launch_gemm_f32_pair(hipStream_t st, const GemmCall& p, const GemmCall& q) {
+  const GemmArgs g0 = make_args(p), g1 = make_args(q);
+  const bool pair = g0.M > 0 && g0.N > 0 && g1.M > 0 && g1.N > 0 && small_tiles(g0) && small_tiles(g1) &&
+                    !g0.a.trans && !g1.a.trans && vec_ok(g0.a, g0.Kd) && vec_ok(g0.b, g0.Kd) &&
+                    vec_ok(g1.a, g1.Kd) && vec_ok(g1.b, g1.Kd);
+  if (!pair) {
+    const int rc = launch_args(st, g0);
+    return rc ? rc : launch_args(st, g1);
+  }
+  GemmDesc d0, d1;
+  const int64_t t0 = describe<64, 64>(g0, d0), t1 = describe<64, 64>(g1, d1);
+  if (!g0.b.trans && !g1.b.trans) launch_pair<false, false>(st, d0, t0, d1, t1);
+  else if (!g0.b.trans) launch_pair<false, true>(st, d0, t0, d1, t1);
+  else if (!g1.b.trans) launch_pair<true, false>(st, d0, t0, d1, t1);
+  else launch_pair<true, true>(st, d0, t0, d1, t1);
+  return check_launch("gemm_f32_pair");
 }
 
 }  // namespace gptq

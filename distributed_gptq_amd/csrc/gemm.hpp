@@ -16,8 +16,28 @@ enum GemmFlags {
   GEMM_C_LOWER = 16      // only C[i][j] with i >= j is computed and written
 };
 
+struct GemmCall {
+  int64_t M, N, Kd;
+  float alpha;
+  const float* A;
+  int64_t lda;
+  bool transA;
+  const float* B;
+  int64_t ldb;
+  bool transB;
+  float beta;
+  float* C;
+  int64_t ldc;
+  int flags;
+};
+
 int launch_gemm_f32(hipStream_t st, int64_t M, int64_t N, int64_t Kd, float alpha, const float* A,
                     int64_t lda, bool transA, const float* B, int64_t ldb, bool transB, float beta,
                     float* C, int64_t ldc, int flags);
+
+// Two products that are independent (neither reads or writes what the other
+// writes).  When both take 64 x 64 tiles they run as one grid, so that their
+// tiles share the CUs and the pair pays one launch; otherwise p, then q.
+int launch_gemm_f32_pair(hipStream_t st, const GemmCall& p, const GemmCall& q);
 
 }  // namespace gptq
