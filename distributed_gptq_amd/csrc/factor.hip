@@ -127,78 +127,136 @@ __device__ __forceinline__ float bperm(int src_lane, float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lane * 4, __builtin_bit_cast(int, v)));
 }
 
-// One wave: D (32 x 32 at sD, lower part) = L L^T and X = L^-1, written back
-// over D and into sXd (zeros above).  Lane l holds the 4 x 4 sub-block
-// (rows 4 (l / 8) + u, columns 4 (l % 8) + v) of the working matrix and of
-// Y (initially I).  Step j: the pivot comes from its lane (v_readlane); the
-// lanes holding column j have L's column j, the lanes holding row j have Y's
-// row j scaled by 1 / L[j][j]; every lane fetches the pieces it needs from
-// them with ds_bpermute and applies the two rank-1 updates
+// One wave: D (B x B at sD, lower part; B = 16 or 32) = L L^T and X = L^-1,
+// written back over D and into sXd (zeros above).  Lane l holds the S x S
+// sub-block (S = B / 8; rows S (l / 8) + u, columns S (l % 8) + v) of the
+// working matrix and of Y (initially I).  Step j: the pivot comes from its
+// lane (v_readlane); the lanes holding column j have L's column j, the lanes
+// holding row j have Y's row j scaled by 1 / L[j][j]; every lane fetches the
+// pieces it needs from them with ds_bpermute and applies the two rank-1
+// updates
 //   D[r][c] -= L[r][j] L[c][j]  (c > j),   Y[r][c] -= L[r][j] Y[j][c]  (r > j),
-// right-looking Cholesky and forward elimination fused.  A column step takes
-// about 600 cycles, most of the leaf; exchanging through LDS instead, or
-// blocking by 4 columns (one exchange and a rank-4 update per 4 columns, same
-// results bit for bit), measured no faster.
-__device__ __forceinline__ void diag32(float* sD, float* sXd, int lane, int col0, int lim, int& first_bad) {
+// right-looking Cholesky and forward elimination fused.  At B = 32 a column
+// step takes about 600 cycles; exchanging through LDS instead, or blocking by
+// 4 columns (one exchange and a rank-4 update per 4 columns, same results bit
+// for bit), measured no faster.
+template <int B>
+__device__ __forceinline__ void diag_blk(float* sD, float* sXd, int lane, int col0, int lim, int& first_bad) {
+  constexpr int S = B / 8;
   const int ra = lane >> 3, cb = lane & 7;
-  float a[4][4], y[4][4];
+  float a[S][S], y[S][S];
 #pragma unroll
-  for (int u = 0; u < 4; ++u)
+  for (int u = 0; u < S; ++u)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      a[u][v] = sD[(4 * ra + u) * kLP + 4 * cb + v];
-      y[u][v] = (4 * ra + u == 4 * cb + v) ? 1.0f : 0.0f;
+    for (int v = 0; v < S; ++v) {
+      a[u][v] = sD[(S * ra + u) * kLP + S * cb + v];
+      y[u][v] = (S * ra + u == S * cb + v) ? 1.0f : 0.0f;
     }
 #pragma unroll
-  for (int j = 0; j < kLB; ++j) {
-    const int jb = j >> 2, jv = j & 3;
+  for (int j = 0; j < B; ++j) {
+    const int jb = j / S, jv = j % S;
     const float piv = rdl(a[jv][jv], jb * 8 + jb);
     if (!(piv > 0.0f) && first_bad < 0 && col0 + j < lim) first_bad = col0 + j;
     // hardware square root and reciprocal (1 ulp): they sit on the
-    // sequential chain of the 32 steps
+    // sequential chain of the B steps
     const float d = __builtin_amdgcn_sqrtf(piv);
     const float id = __builtin_amdgcn_rcpf(d);
-    // column j of L for rows 4 ra + u (kept by the lanes with cb == jb) and
-    // row j of Y for columns 4 cb + v (kept by the lanes with ra == jb);
+    // column j of L for rows S ra + u (kept by the lanes with cb == jb) and
+    // row j of Y for columns S cb + v (kept by the lanes with ra == jb);
     // every lane computes them, the owners' values are broadcast with
     // ds_bpermute (no LDS round trip or wave barrier on the chain)
-    float lv[4], yv[4];
+    float lv[S], yv[S];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int r = 4 * ra + u;
+    for (int u = 0; u < S; ++u) {
+      const int r = S * ra + u;
       lv[u] = r > j ? a[u][jv] * id : (r == j ? d : 0.0f);
       if (cb == jb) a[u][jv] = lv[u];
     }
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
+    for (int v = 0; v < S; ++v) {
       yv[v] = y[jv][v] * id;
       if (ra == jb) y[jv][v] = yv[v];
     }
-    float lr[4], lc[4], yc[4];
+    float lr[S], lc[S], yc[S];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      lr[u] = bperm(8 * ra + jb, lv[u]);  // L[4 ra + u][j]
-      lc[u] = bperm(8 * cb + jb, lv[u]);  // L[4 cb + u][j]
-      yc[u] = bperm(8 * jb + cb, yv[u]);  // Y[j][4 cb + u]
+    for (int u = 0; u < S; ++u) {
+      lr[u] = bperm(8 * ra + jb, lv[u]);  // L[S ra + u][j]
+      lc[u] = bperm(8 * cb + jb, lv[u]);  // L[S cb + u][j]
+      yc[u] = bperm(8 * jb + cb, yv[u]);  // Y[j][S cb + u]
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float lru = 4 * ra + u > j ? lr[u] : 0.0f;
+    for (int u = 0; u < S; ++u) {
+      const float lru = S * ra + u > j ? lr[u] : 0.0f;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        a[u][v] = fmaf(-lr[u], 4 * cb + v > j ? lc[v] : 0.0f, a[u][v]);
+      for (int v = 0; v < S; ++v) {
+        a[u][v] = fmaf(-lr[u], S * cb + v > j ? lc[v] : 0.0f, a[u][v]);
         y[u][v] = fmaf(-lru, yc[v], y[u][v]);
       }
     }
   }
 #pragma unroll
-  for (int u = 0; u < 4; ++u)
+  for (int u = 0; u < S; ++u)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const bool low = 4 * ra + u >= 4 * cb + v;
-      sD[(4 * ra + u) * kLP + 4 * cb + v] = low ? a[u][v] : 0.0f;
-      sXd[(4 * ra + u) * kLP + 4 * cb + v] = low ? y[u][v] : 0.0f;
+    for (int v = 0; v < S; ++v) {
+      const bool low = S * ra + u >= S * cb + v;
+      sD[(S * ra + u) * kLP + S * cb + v] = low ? a[u][v] : 0.0f;
+      sXd[(S * ra + u) * kLP + S * cb + v] = low ? y[u][v] : 0.0f;
     }
+}
+
+// acc += P (16 x 16 at pa, P[r][k] = pa[r * lda + k]) x Q', Q' = Q^T
+// (pb[c * ldb + k]) when bT, else Q (pb[k * ldb + c]); one wave, 4 steps of
+// v_mfma_f32_16x16x4f32 (lane l: operand row/column l % 16, k = 4 s + l / 16)
+__device__ __forceinline__ f32x4 mm16(const float* pa, int lda, const float* pb, int ldb, bool bT, f32x4 acc,
+                                     int lane) {
+  const int i = lane & 15, h = lane >> 4;
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    const int k = 4 * st + h;
+    const float x = pa[i * lda + k];
+    const float y = bT ? pb[i * ldb + k] : pb[k * ldb + i];
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+// 16x16 accumulator layout: lane l, register v -> row 4 (l / 16) + v, column l % 16
+__device__ __forceinline__ int acc16_at(int lane, int v, int ld) { return (4 * (lane >> 4) + v) * ld + (lane & 15); }
+
+// One wave: the 32 x 32 diagonal block at sD (lower part) = L L^T and
+// X = L^-1 into sXd (zeros above), by halves:
+//   L11, Y11 = diag(D11);  L21 = D21 Y11^T;  S = D22 - L21 L21^T;
+//   L22, Y22 = diag(S);    Y21 = -Y22 (L21 Y11)
+// Two 16-column chains take about half the time of one 32-column chain
+// (a 16-column step exchanges and updates a quarter of the elements); the
+// three products are v_mfma_f32_16x16x4f32.  sT: 16 x 17 floats of scratch.
+// The upper 16 x 16 quarter of D is left as it is (the leaf does not read L's
+// diagonal blocks again); that of sXd is never written and stays zero.
+__device__ __forceinline__ void diag32(float* sD, float* sXd, float* sT, int lane, int col0, int lim,
+                                       int& first_bad) {
+  constexpr int H = 16;
+  float* D21 = sD + H * kLP;
+  float* D22 = D21 + H;
+  float* Y21 = sXd + H * kLP;
+  float* Y22 = Y21 + H;
+  diag_blk<H>(sD, sXd, lane, col0, lim, first_bad);
+  f32x4 l21 = {};
+  l21 = mm16(D21, kLP, sXd, kLP, true, l21, lane);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) D21[acc16_at(lane, v, kLP)] = l21[v];
+  f32x4 s = {};
+  s = mm16(D21, kLP, D21, kLP, true, s, lane);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) D22[acc16_at(lane, v, kLP)] -= s[v];
+  diag_blk<H>(D22, Y22, lane, col0 + H, lim, first_bad);
+  f32x4 t = {};
+  t = mm16(D21, kLP, sXd, kLP, false, t, lane);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) sT[acc16_at(lane, v, H + 1)] = t[v];
+  f32x4 y21 = {};
+  y21 = mm16(Y22, kLP, sT, H + 1, false, y21, lane);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) Y21[acc16_at(lane, v, kLP)] = -y21[v];
 }
 
 __global__ __launch_bounds__(256) void chol_inv_leaf(float* __restrict__ A, float* __restrict__ X, int64_t ld,
@@ -244,7 +302,7 @@ __global__ __launch_bounds__(256) void chol_inv_leaf(float* __restrict__ A, floa
   int first_bad = -1;
   auto blk = [&](float* base, int bi, int bj) { return base + bi * kLB * kLP + bj * kLB; };
   for (int kb = 0; kb < NB; ++kb) {
-    if (wave == 0) diag32(blk(sA, kb, kb), blk(sX, kb, kb), lane, kb * kLB, m, first_bad);
+    if (wave == 0) diag32(blk(sA, kb, kb), blk(sX, kb, kb), sS, lane, kb * kLB, m, first_bad);
     __syncthreads();
     // panel: L_ik = A_ik X_kk^T, one wave per block row
     {
