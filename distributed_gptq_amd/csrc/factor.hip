@@ -77,6 +77,42 @@ __global__ void build_A(const float* __restrict__ H, int64_t K, float scale, con
     }
 }
 
+// build_A without Hd, for K <= kRowLdsMax: one workgroup per row i of A
+// stages its source row (H's row perm[K-1-i]) in LDS with 16-byte loads and
+// gathers A[i][0..i] from there (coalesced writes), instead of gathering every
+// element from global memory.  Same arithmetic as build_A.
+constexpr int64_t kRowLdsMax = 32768;
+
+__global__ __launch_bounds__(512) void build_A_rows(const float* __restrict__ H, int64_t K, float scale,
+                                                    const int32_t* __restrict__ perm, int fix_dead,
+                                                    const float* __restrict__ lam, int vec, float* __restrict__ A) {
+  extern __shared__ __attribute__((aligned(16))) float shrow[];
+  const float l = lam[0];
+  const int k = static_cast<int>(K);
+  for (int64_t i = blockIdx.x; i < K; i += gridDim.x) {
+    const int64_t a = K - 1 - i;
+    const float* src = H + (perm ? perm[a] : a) * K;
+    if (vec) {
+      for (int c = 4 * threadIdx.x; c < k; c += 4 * blockDim.x)
+        *reinterpret_cast<f32x4*>(shrow + c) = *reinterpret_cast<const f32x4*>(src + c);
+    } else {
+      for (int c = threadIdx.x; c < k; c += blockDim.x) shrow[c] = src[c];
+    }
+    __syncthreads();
+    float* dst = A + i * K;
+    for (int j = threadIdx.x; j <= i; j += blockDim.x) {
+      const int b = k - 1 - j;
+      float v = scale * shrow[perm ? perm[b] : b];
+      if (j == i) {
+        if (fix_dead && v == 0.0f) v = 1.0f;
+        v += l;
+      }
+      dst[j] = v;
+    }
+    __syncthreads();
+  }
+}
+
 __global__ void fill_zero(float* __restrict__ p, int64_t n) {
   for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x)
@@ -472,9 +508,15 @@ extern "C" int gptq_damp_factor(const float* H, int64_t K, float scale, float pe
   hipLaunchKernelGGL(diag_stats, dim3(1), dim3(1024), 0, st, H, K, scale, percdamp, dead_cols, lam, info);
   int rc = check_launch("diag_stats");
   if (rc) return rc;
-  hipLaunchKernelGGL(build_A, dim3(static_cast<unsigned>(std::min<int64_t>(cdiv(K, 256), 64)),
-                                  static_cast<unsigned>(std::min<int64_t>(K, 65535))),
-                     dim3(256), 0, st, H, K, scale, perm, dead_cols ? 1 : 0, lam, A, Hd);
+  if (!Hd && K <= kRowLdsMax) {
+    const int vec = (reinterpret_cast<uintptr_t>(H) % 16 == 0 && K % 4 == 0) ? 1 : 0;
+    hipLaunchKernelGGL(build_A_rows, dim3(static_cast<unsigned>(K)), dim3(512), sizeof(float) * K, st, H, K, scale,
+                       perm, dead_cols ? 1 : 0, lam, vec, A);
+  } else {
+    hipLaunchKernelGGL(build_A, dim3(static_cast<unsigned>(std::min<int64_t>(cdiv(K, 256), 64)),
+                                    static_cast<unsigned>(std::min<int64_t>(K, 65535))),
+                       dim3(256), 0, st, H, K, scale, perm, dead_cols ? 1 : 0, lam, A, Hd);
+  }
   if ((rc = check_launch("build_A"))) return rc;
   hipLaunchKernelGGL(fill_zero, dim3(grid_for(K * K, 256)), dim3(256), 0, st, out, K * K);
   if ((rc = check_launch("fill_zero"))) return rc;
