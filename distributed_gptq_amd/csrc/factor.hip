@@ -172,10 +172,11 @@ __device__ __forceinline__ float bperm(int src_lane, float v) {
 // pieces it needs from them with ds_bpermute and applies the two rank-1
 // updates
 //   D[r][c] -= L[r][j] L[c][j]  (c > j),   Y[r][c] -= L[r][j] Y[j][c]  (r > j),
-// right-looking Cholesky and forward elimination fused.  At B = 32 a column
-// step takes about 600 cycles; exchanging through LDS instead, or blocking by
-// 4 columns (one exchange and a rank-4 update per 4 columns, same results bit
-// for bit), measured no faster.
+// right-looking Cholesky and forward elimination fused.  The leaf uses B = 16
+// (diag32 below joins two such chains); one B = 32 chain took about 600 cycles
+// a column step, and exchanging through LDS instead, or blocking by 4 columns
+// (one exchange and a rank-4 update per 4 columns, same results bit for bit),
+// measured no faster.
 template <int B>
 __device__ __forceinline__ void diag_blk(float* sD, float* sXd, int lane, int col0, int lim, int& first_bad) {
   constexpr int S = B / 8;
