@@ -167,3 +167,18 @@ def test_factor_reports_not_positive_definite(hip):
     H = -np.eye(K, dtype=np.float32)
     _, _, _, info = _ops.damp_factor(torch.from_numpy(H).cuda(), 1.0, 0.0, None, _lib.FACTOR_FULL_INVERSE)
     assert int(info.item()) > 0
+
+
+@pytest.mark.parametrize("k", [0, 20, 150, 299])
+def test_factor_reports_first_bad_column(hip, k):
+    """info = 1 + the first column (in the factor's reversed order) whose pivot
+    is not positive: a negative entry at column k of an otherwise identity
+    matrix, placed in the first or second 16-column half of a diagonal block,
+    in a later 128-column leaf, and in the padded last leaf (K = 300)."""
+    from distributed_gptq_amd import _lib, _ops
+    K = 300
+    a = np.ones(K, dtype=np.float32)
+    a[k] = -1.0
+    H = np.diag(a[::-1]).copy()  # the factor works on the index-reversed matrix
+    _, _, _, info = _ops.damp_factor(torch.from_numpy(H).cuda(), 1.0, 0.0, None, _lib.FACTOR_UPPER_CHOL_INV)
+    assert int(info.item()) == k + 1
