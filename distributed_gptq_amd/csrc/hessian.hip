@@ -676,16 +676,19 @@ __global__ __launch_bounds__(256) void hessian_reduce(float* __restrict__ H, int
 
 // Token splits.  Every split writes, and the reduce reads back, 512 KB per
 // tile, so splits cost traffic once they are short: at most 16384 tokens per
-// split, and beyond that only as many splits as bring the launch to ~512
-// workgroups while each keeps >= 1024 tokens; at most 64.  Measured on
-// MI355X (fp16 X): (n, K) = (32768, 768) -> 32 splits, (32768, 3072) -> 7,
-// (16384, 5120) -> 3, (16384, 13824) -> 1, (262144, 4096 or 14336) -> 16,
-// each within 5% of the best split count of a sweep over 1..64, and
-// 1.2-1.5x faster than ~2048 workgroups for the short calls.
+// split (10240 for products of fewer than 512 tiles, K < 5888), and beyond
+// that only as many splits as bring the launch to ~512 workgroups while each
+// keeps >= 1024 tokens; at most 64.  Measured on MI355X (fp16 X): (n, K) =
+// (32768, 768) -> 32 splits, (32768, 3072) -> 7, (16384, 5120) -> 3,
+// (16384, 13824) -> 1, (262144, 14336) -> 16, each within 5% of the best split
+// count of a sweep over 1..64, and 1.2-1.5x faster than ~2048 workgroups for
+// the short calls; bf16 at (262144, 4096): 16 / 24 / 32 splits 4.57 / 4.47 /
+// 4.52 ms (26 now).
 int choose_splits(int64_t n, int ntiles) {
-  constexpr int64_t kTokMax = 16384, kTokMin = 1024, kMinWG = 512;
+  constexpr int64_t kTokMin = 1024, kMinWG = 512;
+  const int64_t tok_max = ntiles < 512 ? 10240 : 16384;
   const int64_t fill = std::min<int64_t>(cdiv(kMinWG, static_cast<int64_t>(ntiles)), std::max<int64_t>(1, n / kTokMin));
-  const int64_t s = std::max<int64_t>(cdiv(n, kTokMax), fill);
+  const int64_t s = std::max<int64_t>(cdiv(n, tok_max), fill);
   return static_cast<int>(std::min<int64_t>(std::max<int64_t>(s, 1), 64));
 }
 
