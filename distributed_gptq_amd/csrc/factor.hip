@@ -122,10 +122,11 @@ __global__ void fill_zero(float* __restrict__ p, int64_t n) {
 // One workgroup of 4 waves: Cholesky of the m x m (m <= 128) diagonal block
 // of A at (n0, n0) and the inverse of its factor, blocked by 32:
 //   for each diagonal block k:  one wave factors D_kk = L_kk L_kk^T and
-//     inverts L_kk (X_kk) together (diag32); then L_ik = A_ik X_kk^T (panel)
-//     and A_ij -= L_ik L_jk^T
-//     (trailing) as 32x32x32 v_mfma_f32_32x32x2f32 products, one per wave;
-//   then X_ij (i > j) = -X_ii sum_{k=j}^{i-1} L_ik X_kj by block distance.
+//     inverts L_kk (X_kk) together (diag32) while the others form
+//     S_kj = sum_{i=j}^{k-1} L_ki X_ij for X's row block k; then
+//     X_kj = -X_kk S_kj and the panel L_ik = A_ik X_kk^T, then
+//     A_ij -= L_ik L_jk^T (trailing), as 32x32x32 v_mfma_f32_32x32x2f32
+//     products, one per wave.
 // The tile is padded to 128 with the identity.  Writes X = L^-1 (zeros
 // above) into X (A's block is left as scratch); a non-positive pivot records
 // info = 1 + (column in A order) once.
@@ -306,6 +307,7 @@ __global__ __launch_bounds__(256) void chol_inv_leaf(float* __restrict__ A, floa
   const int lane = tid & 63;
   const int wave = tid >> 6;
   constexpr int NB = kNB / kLB;
+  static_assert(NB == 4, "waves 1..3 form the sums of row blocks 1..3, and each phase has NB - 1 blocks");
 
   // load the lower triangle (identity padding beyond m), 32 loads in flight per thread
   for (int e0 = tid; e0 < kNB * kNB; e0 += 256 * 32) {
@@ -338,16 +340,31 @@ __global__ __launch_bounds__(256) void chol_inv_leaf(float* __restrict__ A, floa
 
   int first_bad = -1;
   auto blk = [&](float* base, int bi, int bj) { return base + bi * kLB * kLP + bj * kLB; };
+  // Row block kb of X off the diagonal, X_kj = -X_kk S_kj with
+  // S_kj = sum_{i=j}^{k-1} L_ki X_ij (j < k), is built in the same loop: waves
+  // 1..kb form S_kb,j (j = wave - 1, into their sS slots) while wave 0 factors
+  // block kb, and the products by X_kk share the panel phase (waves j < kb
+  // take X_kb,j, the others the panel blocks), so no pass follows the loop.
   for (int kb = 0; kb < NB; ++kb) {
-    if (wave == 0) diag32(blk(sA, kb, kb), blk(sX, kb, kb), sS, lane, kb * kLB, m, first_bad);
+    if (wave == 0) {
+      diag32(blk(sA, kb, kb), blk(sX, kb, kb), sS, lane, kb * kLB, m, first_bad);
+    } else if (wave - 1 < kb) {
+      const int jb = wave - 1;
+      f32x16 acc = {};
+      for (int k = jb; k < kb; ++k) acc = mm32(blk(sA, kb, k), kLP, blk(sX, k, jb), kLP, false, acc, lane);
+      put32(sS + wave * kLB * (kLB + 1), kLB + 1, acc, 1.0f, lane);
+    }
     __syncthreads();
-    // panel: L_ik = A_ik X_kk^T, one wave per block row
-    {
-      const int ib = kb + 1 + wave;
-      if (ib < NB) {
-        f32x16 acc = {};
-        acc = mm32(blk(sA, ib, kb), kLP, blk(sX, kb, kb), kLP, true, acc, lane);
-        put32(blk(sA, ib, kb), kLP, acc, 1.0f, lane);
+    // NB - 1 blocks per phase, one per wave: X_kb,j = -X_kk S_kb,j for
+    // j = wave < kb, then the panel L_ib,kb = A_ib,kb X_kk^T for ib = wave + 1 > kb
+    if (wave < NB - 1) {
+      f32x16 acc = {};
+      if (wave < kb) {
+        acc = mm32(blk(sX, kb, kb), kLP, sS + (wave + 1) * kLB * (kLB + 1), kLB + 1, false, acc, lane);
+        put32(blk(sX, kb, wave), kLP, acc, -1.0f, lane);
+      } else {
+        acc = mm32(blk(sA, wave + 1, kb), kLP, blk(sX, kb, kb), kLP, true, acc, lane);
+        put32(blk(sA, wave + 1, kb), kLP, acc, 1.0f, lane);
       }
     }
     __syncthreads();
@@ -366,20 +383,6 @@ __global__ __launch_bounds__(256) void chol_inv_leaf(float* __restrict__ A, floa
             c -= acc[v];
           }
         }
-    }
-    __syncthreads();
-  }
-  // X_ij = -X_ii S, S = sum_{k=j}^{i-1} L_ik X_kj, by block distance
-  for (int d = 1; d < NB; ++d) {
-    const int jb = wave, ib = wave + d;
-    if (ib < NB) {
-      f32x16 acc = {};
-      for (int k = jb; k < ib; ++k) acc = mm32(blk(sA, ib, k), kLP, blk(sX, k, jb), kLP, false, acc, lane);
-      float* ps = sS + wave * kLB * (kLB + 1);
-      put32(ps, kLB + 1, acc, 1.0f, lane);
-      f32x16 acc2 = {};
-      acc2 = mm32(blk(sX, ib, ib), kLP, ps, kLB + 1, false, acc2, lane);
-      put32(blk(sX, ib, jb), kLP, acc2, -1.0f, lane);
     }
     __syncthreads();
   }
