@@ -38,21 +38,36 @@ def _gpu(*ts):
 
 
 _ws: dict = {}
+_ws_in_graph: set = set()   # keys whose current buffer a graph capture has used
+_ws_retired: list = []      # replaced buffers a captured graph may still write
 
 
 def workspace(nbytes: int, device) -> torch.Tensor:
     """Scratch buffer per (device, stream), grown on demand.  Work on one
-    stream is ordered, so reuse across calls is safe."""
-    key = (torch.device(device).index, torch.cuda.current_stream(device).cuda_stream)
+    stream is ordered, so reuse across calls is safe.  A graph captured on
+    the stream bakes the buffer's address into its kernels, so a buffer
+    handed out during a capture is never freed when a later, larger call
+    replaces it: it is kept until ``release_workspaces()``."""
+    dev = torch.device(device)
+    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
     buf = _ws.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        if buf is not None and key in _ws_in_graph:
+            _ws_retired.append(buf)
+            _ws_in_graph.discard(key)
+        buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
         _ws[key] = buf
+    if torch.cuda.is_current_stream_capturing():
+        _ws_in_graph.add(key)
     return buf
 
 
 def release_workspaces():
+    """Drop every cached workspace.  Graphs captured with them must be
+    dropped first."""
     _ws.clear()
+    _ws_in_graph.clear()
+    _ws_retired.clear()
 
 
 # ------------------------------------------------------------- Hessian --

@@ -22,7 +22,11 @@ result) have no ``layers`` entry and load as they are. A file without
 buffer shapes and ``quantization_config.bits``.
 
 Tensors are stored as they are: packed uint8 codes, fp16 scales and zeros,
-int32 g_idx and the bias all round-trip bit-exactly. Loading uses only
+int32 g_idx and the bias all round-trip bit-exactly.  Act-order layers are
+written in the reference's column order (QuantizedLinear's state dict holds
+the codes in input-column order and no ``perm``); loading re-derives the
+serving order from g_idx.  Files from the earlier format with a ``perm`` key
+(codes in that stored order) still load. Loading uses only
 loaders that execute nothing from the file: safetensors, and ``torch.load``
 with ``weights_only=True`` for the pytorch format. The reference writes only
 on rank 0 (:281-283, :288-290); this module runs in one process and always
@@ -182,7 +186,7 @@ def _install(model: nn.Module, name: str, info: dict, state: Dict[str, torch.Ten
         setattr(parent, parts[-1], q)
     else:
         raise TypeError(f"{name}: expected nn.Linear or QuantizedLinear, found {type(old).__name__}")
-    extra = (("bias",) if info["bias"] else ()) + (("perm",) if f"{name}.perm" in state else ())
+    extra = ("bias",) if info["bias"] else ()
     for key in _BUFFERS + extra:
         t = state[f"{name}.{key}"]
         getattr(q, key).data = torch.empty(t.shape, dtype=t.dtype, device=device)

@@ -1170,8 +1170,10 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
       uint32_t pr[4][4];
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) step_pairs<BITS>(L.cw[i], kk, pr[kk]);
-      // GPTQ zero points are integers: the packed path (fp16), chosen for the whole wave
-      if (!BF16 && __all(z == rintf(z) && z >= 0.0f && z <= 1023.0f)) {
+      // GPTQ zero points are integers: the packed path (fp16 activations and
+      // fp16 scales, so that s is exact in fp16 and (q - z) * s rounds once),
+      // chosen for the whole wave
+      if (!BF16 && a.sz_dtype == GPTQ_F16 && __all(z == rintf(z) && z >= 0.0f && z <= 1023.0f)) {
         const uint32_t zz = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(1024.0f + z),
                                                                 static_cast<_Float16>(1024.0f + z)});
         const uint32_t sh = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(s), static_cast<_Float16>(s)});
@@ -1583,10 +1585,11 @@ __global__ __launch_bounds__(64 * (WAVES + L)) __attribute__((amdgpu_waves_per_e
       return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, fa), __builtin_bit_cast(f16x8, fb), c, 0,
                                                     0, 0);
   };
-  // GPTQ zero points are integers: with fp16 activations and every zero of
-  // the wave's rows an integer in [0, 1023] the decode is packed fp16 math
+  // GPTQ zero points are integers: with fp16 activations, fp16 scales (exact
+  // in the packed multiply, so (q - z) * s rounds once) and every zero of the
+  // wave's rows an integer in [0, 1023] the decode is packed fp16 math
   // ((1024 + q) - (1024 + z) exact, then * s), decided once
-  bool pk = !BF16;
+  bool pk = !BF16 && a.sz_dtype == GPTQ_F16;
   if constexpr (!BF16) {
     for (int64_t g = g4; g < a.ngroups; g += 4)
 #pragma unroll

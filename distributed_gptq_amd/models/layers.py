@@ -22,7 +22,11 @@ weight column j holds input column perm[j], stored so that groups are
 contiguous (g_idx[perm[j]] = j // group_size): the layer is then served by
 the same fast kernels, x gathered through perm, instead of a per-weight
 group lookup.  The operator takes it as an optional last argument, so the
-reference's six-argument call is unchanged.
+reference's six-argument call is unchanged.  ``perm`` is not part of the
+state dict: ``state_dict()`` writes qweight in input-column order (the
+reference's layout, so its strict ``load_state_dict`` takes the file), and
+loading re-derives perm as the stable sort of g_idx, as ``pack_weights``
+does, and reorders the codes again.
 """
 from __future__ import annotations
 
@@ -101,6 +105,54 @@ def _group_layout(g_idx: torch.Tensor, K: int, ngroups: int, perm: Optional[torc
 # Llama-3-8B and 13B layer shapes): at 384 rows the two are even or the GEMM
 # wins, at 512 it wins everywhere, at 16384 rows by 3.4-3.7x.
 DEQUANT_GEMM_ROWS = 384
+
+
+def _unpack_rows(qweight: torch.Tensor, bits: int, K: int) -> torch.Tensor:
+    """(N, K) uint8 codes of LSB-first b-bit rows (any device; byte ops
+    only -- a checkpoint's storage order, not the compute path)."""
+    N = qweight.shape[0]
+    if bits in (2, 4, 8):
+        per = 8 // bits
+        sh = torch.arange(0, 8, bits, device=qweight.device, dtype=torch.uint8)
+        c = (qweight.unsqueeze(-1) >> sh) & ((1 << bits) - 1)
+        return c.reshape(N, -1)[:, :K].contiguous() if per > 1 else qweight[:, :K].contiguous()
+    sh = torch.arange(8, device=qweight.device, dtype=torch.uint8)
+    b = ((qweight.unsqueeze(-1) >> sh) & 1).reshape(N, -1)[:, :K * bits].reshape(N, K, bits)
+    out = b[..., 0].clone()
+    for i in range(1, bits):
+        out |= b[..., i] << i
+    return out
+
+
+def _pack_rows(codes: torch.Tensor, bits: int) -> torch.Tensor:
+    """Inverse of ``_unpack_rows``: ceil(K * bits / 8) bytes per row."""
+    N, K = codes.shape
+    pitch = (K * bits + 7) // 8
+    if bits in (2, 4, 8):
+        per = 8 // bits
+        c = torch.zeros(N, pitch * per, device=codes.device, dtype=torch.uint8)
+        c[:, :K] = codes
+        c = c.reshape(N, pitch, per)
+        out = c[..., 0].clone()
+        for i in range(1, per):
+            out |= c[..., i] << (bits * i)
+        return out
+    sh = torch.arange(bits, device=codes.device, dtype=torch.uint8)
+    b = torch.zeros(N, pitch * 8, device=codes.device, dtype=torch.uint8)
+    b[:, :K * bits] = ((codes.unsqueeze(-1) >> sh) & 1).reshape(N, -1)
+    b = b.reshape(N, pitch, 8)
+    out = b[..., 0].clone()
+    for i in range(1, 8):
+        out |= b[..., i] << i
+    return out
+
+
+def _gather_code_columns(qweight: torch.Tensor, bits: int, packed: bool, K: int, idx: torch.Tensor) -> torch.Tensor:
+    """Stored codes with column j of the result taken from column idx[j]."""
+    idx = idx.to(device=qweight.device).long()
+    if not packed or bits == 8:
+        return qweight[:, idx].contiguous()
+    return _pack_rows(_unpack_rows(qweight, bits, K)[:, idx], bits)
 
 
 def _linear_impl(x, qweight, scales, zeros, g_idx, bias, perm=None):
@@ -199,11 +251,24 @@ class QuantizedLinear(nn.Module):
         self.register_buffer("scales", torch.zeros((out_features, self.num_groups), dtype=torch.float16))
         self.register_buffer("zeros", torch.zeros((out_features, self.num_groups), dtype=torch.float16))
         self.register_buffer("g_idx", torch.arange(in_features, dtype=torch.int32) // self.group_size)
-        self.register_buffer("perm", torch.zeros(0, dtype=torch.int32))
+        self.register_buffer("perm", torch.zeros(0, dtype=torch.int32), persistent=False)
         if bias:
             self.register_parameter("bias", nn.Parameter(torch.zeros(out_features)))
         else:
             self.register_parameter("bias", None)
+
+    def _contiguous_order(self, gi: torch.Tensor) -> Optional[torch.Tensor]:
+        """The stored column order that makes an act-order g_idx's groups
+        contiguous (the stable sort of g_idx), or None when g_idx already is
+        k // group_size or no order makes it so."""
+        ar = torch.arange(self.in_features, dtype=torch.int32, device=gi.device)
+        contiguous = ar // self.group_size
+        if bool(torch.equal(gi, contiguous)):
+            return None
+        cand = torch.argsort(gi, stable=True).to(torch.int32)
+        if bool(torch.equal(gi[cand.long()], contiguous)):
+            return cand
+        return None
 
     def pack_weights(self, weight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor,
                      g_idx: Optional[torch.Tensor] = None, perm: Optional[torch.Tensor] = None):
@@ -219,11 +284,8 @@ class QuantizedLinear(nn.Module):
         if g_idx is not None:
             self.g_idx.data = g_idx.to(torch.int32).to(dev)
         ar = torch.arange(self.in_features, dtype=torch.int32, device=dev)
-        gi = self.g_idx.to(dev)
-        if perm is None and not bool(torch.equal(gi, ar // self.group_size)):
-            cand = torch.argsort(gi, stable=True).to(torch.int32)
-            if bool(torch.equal(gi[cand.long()], ar // self.group_size)):
-                perm = cand
+        if perm is None:
+            perm = self._contiguous_order(self.g_idx.to(dev))
         if perm is not None:
             perm = perm.to(device=dev, dtype=torch.int32)
             if bool(torch.equal(perm, ar)):
@@ -246,27 +308,47 @@ class QuantizedLinear(nn.Module):
             return torch.ops.gptq.linear(x, self.qweight, self.scales, self.zeros, self.g_idx, self.bias, self.perm)
         return torch.ops.gptq.linear(x, self.qweight, self.scales, self.zeros, self.g_idx, self.bias)
 
+    def _save_to_state_dict(self, destination, prefix, keep_vars):
+        # the reference's layout: codes in input-column order, no perm
+        super()._save_to_state_dict(destination, prefix, keep_vars)
+        if self.perm.numel():
+            inv = torch.argsort(self.perm.long())  # input column k sits at stored column inv[k]
+            destination[prefix + "qweight"] = _gather_code_columns(self.qweight.detach(), self.bits, self.packed,
+                                                                   self.in_features, inv)
+
     def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
                               error_msgs):
-        # perm has K entries with act-order and none otherwise; the
-        # reference's checkpoints have no perm at all (identity)
+        # Files hold qweight in input-column order (the reference's layout,
+        # and what state_dict() writes); files written with a ``perm`` key
+        # (K entries) hold it in that stored order instead.
         key = prefix + "perm"
         saved = state_dict.get(key)
-        if saved is not None and saved.shape != self.perm.shape:
-            self.perm.data = torch.empty(saved.shape, dtype=torch.int32, device=self.perm.device)
         super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
                                       error_msgs)
-        if saved is None:
-            if key in missing_keys:
-                missing_keys.remove(key)
-            self.perm.data = torch.zeros(0, dtype=torch.int32, device=self.perm.device)
-        # the reference's placeholder g_idx = arange(K) (models/layers.py:60)
-        # means contiguous groups of group_size
+        if key in unexpected_keys:
+            unexpected_keys.remove(key)
+        dev = self.qweight.device
         K = self.in_features
-        if self.num_groups != K and self.g_idx.numel() == K and not self.perm.numel():
-            ar = torch.arange(K, dtype=torch.int32, device=self.g_idx.device)
-            if bool(torch.equal(self.g_idx.to(torch.int32), ar)):
-                self.g_idx.data = ar // self.group_size
+        if saved is not None and saved.numel():
+            if saved.shape != (K,):
+                error_msgs.append(f"{key}: saved shape {tuple(saved.shape)}, expected (0,) or ({K},)")
+                return
+            self.perm.data = saved.to(device=dev, dtype=torch.int32).contiguous()
+            return
+        self.perm.data = torch.zeros(0, dtype=torch.int32, device=dev)
+        if self.g_idx.numel() != K:
+            return
+        gi = self.g_idx.to(torch.int32)
+        ar = torch.arange(K, dtype=torch.int32, device=gi.device)
+        if self.num_groups != K and bool(torch.equal(gi, ar)):
+            # the reference's placeholder g_idx = arange(K) (models/layers.py:60)
+            # means contiguous groups of group_size
+            self.g_idx.data = ar // self.group_size
+            return
+        perm = self._contiguous_order(gi)
+        if perm is not None:
+            self.qweight.data = _gather_code_columns(self.qweight, self.bits, self.packed, K, perm)
+            self.perm.data = perm.to(dev).contiguous()
 
     @classmethod
     def from_linear(cls, linear_layer: nn.Linear, bits: int = 4, group_size: int = 128,

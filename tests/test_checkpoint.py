@@ -235,3 +235,108 @@ def test_gptq_layers_round_trip_forward_bit_exact(hip, tmp_path, fmt):
         x = torch.randn(5, a.in_features, device="cuda", generator=g).half()
         with torch.no_grad():
             assert torch.equal(a(x), b(x)), name
+
+
+# ------------------------------------------------ act-order column order --
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+@pytest.mark.parametrize("K", [7, 64, 200])
+def test_code_row_packing_matches_the_oracle(bits, K):
+    """The byte-level unpack / pack behind the act-order column reorder of a
+    checkpoint: LSB-first b-bit rows, as the oracle packs them."""
+    from distributed_gptq_amd.models.layers import _pack_rows, _unpack_rows
+    from oracle import gptq_oracle as O
+    import numpy as np
+    codes = np.random.default_rng(bits * K).integers(0, 2 ** bits, (5, K)).astype(np.uint8)
+    packed = O.pack_bitstream(codes, bits)
+    assert torch.equal(_pack_rows(torch.from_numpy(codes), bits), torch.from_numpy(packed))
+    assert torch.equal(_unpack_rows(torch.from_numpy(packed), bits, K), torch.from_numpy(codes))
+
+
+class RefQuantizedLinear(nn.Module):
+    """Only the reference's QuantizedLinear buffers (models/layers.py:49-60):
+    qweight, fp16 scales / zeros, int32 g_idx, bias."""
+
+    def __init__(self, row_bytes, K, N, ngroups, bias):
+        super().__init__()
+        self.register_buffer("qweight", torch.zeros((N, row_bytes), dtype=torch.uint8))
+        self.register_buffer("scales", torch.zeros((N, ngroups), dtype=torch.float16))
+        self.register_buffer("zeros", torch.zeros((N, ngroups), dtype=torch.float16))
+        self.register_buffer("g_idx", torch.arange(K, dtype=torch.int32))
+        self.bias = nn.Parameter(torch.zeros(N)) if bias else None
+
+
+def _actorder_layer(bits, gs, K, N, seed, packed=True):
+    """A QuantizedLinear holding act-order codes the way from_gptq stores
+    them (columns in perm order, perm = stable sort of g_idx), built on the
+    CPU with the oracle's packing; returns it and the input-order codes."""
+    import numpy as np
+
+    from distributed_gptq_amd.models.layers import QuantizedLinear
+    from oracle import gptq_oracle as O
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(0, 2 ** bits, (N, K)).astype(np.uint8)
+    sweep = rng.permutation(K)
+    g_idx = np.empty(K, np.int32)
+    g_idx[sweep] = np.arange(K) // gs
+    perm = np.argsort(g_idx, kind="stable").astype(np.int32)
+    q = QuantizedLinear(bits, gs, K, N, bias=True, packed=packed)
+    stored = codes[:, perm]
+    q.qweight.data = torch.from_numpy(O.pack_bitstream(stored, bits) if q.packed else stored.copy())
+    q.scales.data = torch.from_numpy(rng.uniform(1e-3, 1e-2, q.scales.shape)).half()
+    q.zeros.data = torch.from_numpy(rng.integers(0, 2 ** bits, q.zeros.shape).astype(np.float64)).half()
+    q.g_idx.data = torch.from_numpy(g_idx)
+    q.perm.data = torch.from_numpy(perm)
+    q.bias.data = torch.randn(N)
+    return q, codes
+
+
+@pytest.mark.parametrize("bits,gs,packed", [(4, 16, True), (3, 32, True), (2, 16, False), (8, 16, False)])
+def test_actorder_checkpoint_loads_strictly_into_reference_modules(tmp_path, bits, gs, packed):
+    """A saved act-order layer has the reference's keys only (no perm) and its
+    codes in input-column order: a strict load_state_dict into modules with
+    only the reference's buffers (core/quantizer.py:319-320) takes it and
+    decodes the same weights; loading it back into this package's
+    QuantizedLinear re-derives perm and the stored order bit for bit."""
+    import numpy as np
+    from safetensors.torch import load_file
+
+    from distributed_gptq_amd import load_quantized_model, save_quantized_model
+    from oracle import gptq_oracle as O
+    model = Model(seed=4)
+    lin = _get(model, "layers.0.mlp.0")
+    q, codes = _actorder_layer(bits, gs, lin.in_features, lin.out_features, seed=bits, packed=packed)
+    _set(model, "layers.0.mlp.0", q)
+    path = tmp_path / "m.safetensors"
+    save_quantized_model(model, path)
+    state = load_file(str(path))
+    assert "layers.0.mlp.0.perm" not in state
+    ref_model = Model(seed=5)
+    _set(ref_model, "layers.0.mlp.0", RefQuantizedLinear(q.qweight.shape[1], q.in_features, q.out_features,
+                                                         q.num_groups, bias=True))
+    ref_model.load_state_dict(state, strict=True)
+    rq = _get(ref_model, "layers.0.mlp.0")
+    expect = O.pack_bitstream(codes, bits) if q.packed else codes
+    np.testing.assert_array_equal(rq.qweight.numpy(), expect)
+    got = O.unpack_bitstream(rq.qweight.numpy(), bits, q.in_features) if q.packed else rq.qweight.numpy()
+    gi = rq.g_idx.numpy()
+    np.testing.assert_array_equal(O.dequant(got, rq.scales.numpy(), rq.zeros.numpy(), gi),
+                                  O.dequant(codes, q.scales.numpy(), q.zeros.numpy(), q.g_idx.numpy()))
+    # back into this package's layer: perm and the stored order return
+    dst = load_quantized_model(Model(seed=6), path)
+    back = _get(dst, "layers.0.mlp.0")
+    assert torch.equal(back.perm, q.perm) and torch.equal(back.qweight, q.qweight)
+    assert torch.equal(back.g_idx, q.g_idx) and torch.equal(back.scales, q.scales)
+
+
+def test_checkpoint_with_a_perm_key_still_loads(tmp_path):
+    """The earlier format (a ``perm`` key, codes in that stored order) loads
+    into the same layer."""
+    from distributed_gptq_amd.models.layers import QuantizedLinear
+    q, _ = _actorder_layer(4, 16, 64, 48, seed=9)
+    sd = {k: v.clone() for k, v in q.state_dict().items()}
+    sd["qweight"] = q.qweight.clone()
+    sd["perm"] = q.perm.clone()
+    fresh = QuantizedLinear(4, 16, 64, 48, bias=True)
+    fresh.load_state_dict(sd, strict=True)
+    assert torch.equal(fresh.perm, q.perm) and torch.equal(fresh.qweight, q.qweight)

@@ -100,3 +100,50 @@ def test_hessian_graph_replays_accumulate_like_eager(hip, n, K, dt):
         _ops.hessian_accumulate(other, X2)  # eager work between the replays
         torch.cuda.synchronize()
         assert torch.equal(Hg, snaps[r]), r
+
+
+def test_graph_workspace_survives_a_larger_eager_call(hip):
+    """A graph captured with the stream's cached workspace (split-K partial
+    sums), then an eager call on the same stream that needs more space and
+    so replaces the cached buffer, then other tensors allocated and filled:
+    the captured buffer must stay alive, so replays still equal the eager
+    result and the other tensors keep their values."""
+    from distributed_gptq_amd import _ops
+    M, N, K, bits, gs = 64, 4096, 4096, 4, 128         # register kernels, K ranges in the workspace (8.4 MB)
+    packed, scales, zeros, perm, bias, xs = _inputs(M, N, K, bits, gs, False, 7)
+    big = _inputs(128, 4096, 4096, 3, 128, False, 8)  # twice the partial sums (16.8 MB)
+    lib = hip
+    assert lib.gptq_linear_workspace_size(128, N, K, 3, gs, 1, 0) > lib.gptq_linear_workspace_size(M, N, K, bits,
+                                                                                                   gs, 1, 0) > 0
+
+    def op(x, out=None):
+        return _ops.linear(x, packed, bits, scales, zeros, K, group_size=gs, bias=bias, out=out)
+
+    eager = op(xs[0])
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    y = torch.empty(M, N, dtype=torch.float16, device="cuda")
+    with torch.cuda.stream(s):
+        op(xs[0], out=y)
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            op(xs[0], out=y)
+        # a larger call on the same stream grows (replaces) its workspace
+        bp, bs, bz, _, bb, bx = big
+        yb = _ops.linear(bx[0], bp, 3, bs, bz, K, group_size=128, bias=bb)
+        s.synchronize()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    yb_ref = yb.clone()
+    fill = [torch.full((1 << 20,), float(i), device="cuda") for i in range(64)]  # 256 MB of other tensors
+    for r in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager), r
+        for i, t in enumerate(fill):
+            assert bool((t == float(i)).all()), (r, i)
+    assert torch.equal(yb, yb_ref)

@@ -13,12 +13,12 @@
   configs.
 
 Bars: H within 1e-5 relative (Frobenius); U within 2e-5 of the fp64 factor;
-codes agree on >= 99.9% (config 1 against the fp64 oracle; the large-K
-slices: every code the correct rounding of the fp64 replay of the GPU's own
-trajectory to 1e-3 of a step, and free-running agreement with fp64 at least
-that of the fp32 oracle, capped at 99.9%); scales within 1e-5 relative, zero
-points equal except on rounding ties; ||WX - QX||^2 within 1% of the fp64
-oracle's.
+codes agree on >= 99.9% (config 1 against the fp64 oracle; each large-K
+slice against the fp32 oracle or the fp64 oracle, whichever agrees more --
+the two oracles themselves differ by up to 4% on 8-bit zero-point ties --
+plus every code the correct rounding of the fp64 replay of the GPU's own
+trajectory to 1e-3 of a step); scales within 1e-5 relative, zero points equal
+except on rounding ties; ||WX - QX||^2 within 1% of the fp64 oracle's.
 """
 import numpy as np
 import pytest
@@ -203,8 +203,14 @@ def test_sweep_slice_large_K(hip, K, bits, gs, actorder):
       GPU's (scales 1e-5; zero points equal, or one apart where -xmin / s
       sits on a rounding tie: bf16 weights put it exactly on k + 1/2 often,
       e.g. every symmetric range, and fp32 and fp64 then round differently);
-    * free-running, against the oracle in fp32 (the reference's precision):
-      codes agree on >= 99.9%;
+    * free-running: codes agree on >= 99.9% with the oracle in fp32 (the
+      reference's precision, core/gptq.py:88-89, :122) or with the oracle in
+      fp64, whichever agrees more.  Both bars are needed: at 4-bit, K = 13824
+      the fp32 oracle's own codes differ from fp64's on 0.22% (act-order
+      makes every error propagate further) and the GPU's sit between them
+      (99.86% / 99.92%); at 8-bit per-channel a zero point on a rounding tie
+      shifts a whole row, so fp32 and fp64 differ on 1-4% and the GPU agrees
+      with fp32 (99.92%);
     * ||WX - QX||^2 within 1% of the fp64 oracle's."""
     from distributed_gptq_amd import GPTQ
     H, H64, ns = _big(K)
@@ -246,9 +252,10 @@ def test_sweep_slice_large_K(hip, K, bits, gs, actorder):
           f"zero ties {int((dz == 1).sum())}, codes vs fp32 oracle {a32:.6f}, vs fp64 {a64:.6f}, "
           f"fp32 vs fp64 oracle {a3264:.6f}")
     # free-running: one different rounding changes every later error of its
-    # row, so agreement is bounded by arithmetic precision; the GPU agrees
-    # with fp64 at least as closely as the reference's fp32 arithmetic does
-    # (zero points on ties included)
+    # row, so agreement is bounded by arithmetic precision
+    assert max(a32, a64) >= 0.999, (a32, a64, a3264)
+    # and the GPU agrees with fp64 at least as closely as the reference's
+    # fp32 arithmetic does (zero points on ties included)
     assert a64 >= min(0.999, a3264 - 0.002), (a64, a3264)
     # ||WX - QX||^2 of the quantized weights s (q - z) in fp64 (the layer
     # holds them rounded to bf16, an error as large as 8-bit quantization's)
