@@ -17,9 +17,10 @@ placeholder arange(K) (:60, unused by its own unpack) is read as contiguous
 groups of ``group_size`` (rewritten to arange(K) // group_size when loaded).
 
 One buffer is added: ``perm`` (int32).  Empty, the weight columns are in
-input order.  With act-order (GPTQ's sweep order) it holds K entries and
-weight column j holds input column perm[j], stored so that groups are
-contiguous (g_idx[perm[j]] = j // group_size): the layer is then served by
+input order.  With act-order it holds K entries and weight column j holds
+input column perm[j], stored so that groups are contiguous (g_idx[perm[j]]
+= j // group_size; perm is the stable sort of g_idx, i.e. within a group the
+input columns ascend): the layer is then served by
 the same fast kernels, x gathered through perm, instead of a per-weight
 group lookup.  The operator takes it as an optional last argument, so the
 reference's six-argument call is unchanged.  ``perm`` is not part of the
@@ -274,22 +275,25 @@ class QuantizedLinear(nn.Module):
                      g_idx: Optional[torch.Tensor] = None, perm: Optional[torch.Tensor] = None):
         """Store integer codes (N, K, input-column order) and fp16
         scales/zeros (:67-96).  With an act-order ``g_idx`` (groups out of
-        input order) the columns are stored in ``perm`` order, the order
-        that makes the groups contiguous (given, or the stable sort of
-        g_idx); ``g_idx`` itself keeps its meaning (group of input column k)."""
+        input order) the columns are stored in the order that makes the
+        groups contiguous: the stable sort of g_idx, the order a loaded
+        checkpoint re-derives (a given ``perm``, e.g. GPTQ's sweep order,
+        must make the groups contiguous too; it is replaced by that order,
+        which holds the same groups).  ``g_idx`` itself keeps its meaning
+        (group of input column k)."""
         codes = weight.to(torch.uint8)
         dev = codes.device
         self.scales.data = scales.to(torch.float16).reshape(self.out_features, -1).contiguous()
         self.zeros.data = zeros.to(torch.float16).reshape(self.out_features, -1).contiguous()
         if g_idx is not None:
             self.g_idx.data = g_idx.to(torch.int32).to(dev)
-        ar = torch.arange(self.in_features, dtype=torch.int32, device=dev)
-        if perm is None:
-            perm = self._contiguous_order(self.g_idx.to(dev))
+        gi = self.g_idx.to(dev)
         if perm is not None:
-            perm = perm.to(device=dev, dtype=torch.int32)
-            if bool(torch.equal(perm, ar)):
-                perm = None
+            perm = perm.to(device=dev, dtype=torch.long)
+            contiguous = torch.arange(self.in_features, dtype=torch.int32, device=dev) // self.group_size
+            if perm.numel() != self.in_features or not bool(torch.equal(gi[perm], contiguous)):
+                raise ValueError("pack_weights: perm does not make the groups of g_idx contiguous")
+        perm = self._contiguous_order(gi)
         if perm is not None:
             codes = codes[:, perm.long()]
             self.perm.data = perm.contiguous()

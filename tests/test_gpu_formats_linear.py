@@ -623,7 +623,10 @@ def test_quantized_linear_actorder_is_served_fast(hip, bits, gs, M):
     q.add_batch(X)
     q.fasterquant()
     ql = Lm.QuantizedLinear.from_gptq(q)
-    assert ql.perm.numel() == K and torch.equal(ql.perm, q.perm)
+    # stored in the canonical act-order layout: the stable sort of g_idx, which
+    # holds GPTQ's groups (the sweep order's) with input columns ascending in each
+    assert ql.perm.numel() == K and torch.equal(ql.perm, torch.argsort(q.g_idx, stable=True).to(torch.int32))
+    assert torch.equal(q.g_idx[ql.perm.long()], torch.arange(K, device="cuda", dtype=torch.int32) // gs)
     assert Lm._group_layout(ql.g_idx, K, ql.num_groups, ql.perm) == (gs, None)
     Wd = ql.unpack_weights()
     np.testing.assert_array_equal(Wd.cpu().numpy(), O.dequant(
