@@ -174,7 +174,15 @@ def _linear_impl(x, qweight, scales, zeros, g_idx, bias, perm=None):
                 Wi = torch.empty_like(W)
                 Wi[:, perm.long()] = W
                 W = Wi
-        return torch.nn.functional.linear(x, W, None if bias is None else bias.to(x.dtype))
+        # fp32 accumulation and output, the bias added in fp32, one rounding to
+        # x's dtype (a 16-bit product may otherwise reduce split-K partials in
+        # 16 bits, torch's allow_*_reduced_precision_reduction default)
+        x2 = x.reshape(-1, K)
+        if bias is None:
+            y = torch.mm(x2, W.t(), out_dtype=torch.float32)
+        else:
+            y = torch.addmm(bias.to(torch.float32), x2, W.t(), out_dtype=torch.float32)
+        return y.to(x.dtype).reshape(*x.shape[:-1], W.shape[0])
     return _ops.linear(x, qweight, bits, scales, zeros, K, g_idx=gi, group_size=gs, bias=bias, perm=perm)
 
 

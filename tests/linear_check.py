@@ -13,12 +13,20 @@ HIP kernels compute one of two things, per call:
 Both accumulate in fp32 and round the result once to x's dtype.  So each
 output element must lie within
 
-    1/2 ulp_out(|ref| + acc)  +  acc,    acc = K * 2^-24 * (sum_k |x_k| |w_k| + |bias|)
+    1/2 ulp_out(|ref| + acc)  +  acc,    acc = d * 2^-24 * (sum_k |x_k| |w_k| + |bias|)
 
-of the fp64 value ``ref`` of the same semantics (acc is the standard worst-
-case bound of a K-term fp32 dot product, Higham's gamma_K, on the dequantised
-products).  A call passes when every element is inside the bound of one of the
-two semantics.  The checker then plants one wrong code (the top bit of the
+of the fp64 value ``ref`` of the same semantics.  acc is the worst-case bound
+of an fp32 sum in which no term passes through more than d roundings
+(Higham's gamma_d; a K-term sum in one sequential chain has d = K - 1).  These
+kernels sum K products in chains of MFMA or dot steps: an MFMA adds k >= 8
+products (k = 8-32) to its accumulator, so a product passes through at most
+k - 1 roundings inside its step and one per later step, K / k + k in all,
+then the cross-lane, cross-wave and split-K reductions (at most 6 + 4 + 8
+levels), the per-group zero-point correction and the bias; the generic
+kernel sums K / 64 terms per lane, then 6 levels.  d = K / 8 + 128 bounds
+every one of these, and the library GEMM of the many-row route (fp32
+accumulation through MFMAs of k >= 8, fp32 output).  A call passes when every
+element is inside the bound of one of the two semantics.  The checker then plants one wrong code (the top bit of the
 code flipped where |x| * scale is largest) into the oracle's input and
 requires that the same output now fails the bound: that shows the bound is
 tight enough to see a single wrong code.
@@ -71,7 +79,7 @@ def _margins(y, x, W, bias, K, odt):
     if bias is not None:
         ref = ref + bias
         mag = mag + bias.abs()
-    acc = K * U32 * mag
+    acc = (K / 8 + 128) * U32 * mag
     bound = 0.5 * ulp(ref.abs() + acc, odt) + acc
     return (y - ref).abs() / bound, ref, bound
 
