@@ -11,14 +11,19 @@ updates, and packing of all seven layers.  Inputs (calibration activations
 and weights) are resident in HBM before timing starts.
 
 The JSON line also reports the Hessian kernel against the bf16 MFMA
-roofline, the W4A16 / W3A16 dequant-GEMV microbench (M = 1, rotating >= 1 GiB
-of distinct weight buffers so HBM, not the 256 MB last-level cache, is
-measured) and a CPU baseline: the CPU oracle timed on a bounded sample on
-this host's cores and extrapolated to one block.
+roofline; config 4, the W4A16 / W3A16 dequant-GEMV/GEMM microbench (M = 1,
+16, 128, rotating >= 1 GiB of distinct weight buffers so HBM, not the 256 MB
+last-level cache, is measured) beside what a read-only launch of the same
+bytes achieves; config 1 (one Linear(768, 768), s per layer), config 2 (the
+OPT-125m-shaped model) and config 5 (the 13B-shaped model at 4-bit g128
+act-order, one pass and block by block), each wall time and peak HBM; and a
+CPU baseline: the CPU oracle on this host's cores, config 1 and config 4's
+fallback forward in full, the block extrapolated from measured samples.
 
-    python bench.py [--steps 3] [--warmup 1] [--no-cpu] [--no-gemv]
-    python bench.py --workload opt125m     # config 2: whole OPT-125m-shaped model
-    python bench.py --workload llama13b    # config 5: whole 13B-shaped model, 2/4/8 bits
+    python bench.py [--steps 3] [--warmup 1] [--no-cpu] [--no-gemv] [--no-models]
+    python bench.py --workload opt125m     # config 2 alone
+    python bench.py --workload llama13b    # config 5 alone, 2/4/8 bits
+    python bench.py --workload kernels     # the kernel set the counter summaries cover
 """
 from __future__ import annotations
 
@@ -395,6 +400,112 @@ def run_fused(args, torch, dev, bits=4, M=1, min_bytes=1 << 30, reps=3):
     return out
 
 
+def run_read_ceiling(torch, dev, min_bytes=1 << 30, reps=3):
+    """What one launch can read: gptq_stream_read (16-byte non-temporal loads,
+    grid-stride) over each config-4 shape's W4A16 M = 1 byte count, in a HIP
+    graph rotating >= 1 GiB of distinct buffers like the GEMV rows; best of
+    5 grid sizes x 4 unroll depths."""
+    import ctypes
+
+    from distributed_gptq_amd import _lib
+    lib = _lib.lib()
+    out = {}
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    for (N, K) in GEMV_SHAPES:
+        nbytes = gemv_bytes(N, K, 4, 1)
+        pitch = (nbytes + 255) // 256 * 256
+        R = max(2, math.ceil(min_bytes / nbytes))
+        buf = torch.randint(0, 255, (R * pitch,), device=dev, dtype=torch.uint8)
+        best = None
+        for blocks in (256, 512, 1024, 2048, 4096):
+            for unroll in (1, 2, 4, 8):
+                def body():
+                    st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+                    for r in range(R):
+                        _lib.check(lib.gptq_stream_read(ctypes.c_void_p(buf.data_ptr() + r * pitch), nbytes,
+                                                        blocks, unroll, ctypes.c_void_p(flag.data_ptr()), st),
+                                   "gptq_stream_read")
+                s = torch.cuda.Stream(device=dev)
+                s.wait_stream(torch.cuda.current_stream(dev))
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.stream(s):
+                    body()
+                    s.synchronize()
+                    with torch.cuda.graph(graph, stream=s):
+                        body()
+                torch.cuda.current_stream(dev).wait_stream(s)
+                graph.replay()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(reps):
+                    graph.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / (reps * R)
+                if best is None or us < best["us"]:
+                    best = {"us": round(us, 3), "GBps": round(nbytes / us * 1e-3, 1), "bytes": nbytes,
+                            "blocks": blocks, "unroll": unroll, "buffers": R}
+                del graph
+        out[f"{N}x{K}"] = best
+        del buf
+        torch.cuda.empty_cache()
+    return out
+
+
+def run_c1(torch, dev, reps=3):
+    """Config 1 on the GPU: GPTQ of Linear(768, 768) (fp32, W ~ N(0, 0.02^2),
+    seed 0) from 128 add_batch calls of (1, 512, 768) fp32 tokens with 8
+    outlier channels x 20, 4-bit g128, to packed codes: reference mode
+    (GPTQ.quantize + GPTQ.pack_weights, core/gptq.py:63-266) and canonical
+    mode (GPTQ.fasterquant + the packed int32 QuantizedLinear).  Inputs are
+    resident on the GPU; one warm-up, then the median of ``reps`` runs, each
+    phase closed by a device synchronisation."""
+    from distributed_gptq_amd import GPTQ
+    from distributed_gptq_amd.models.layers import QuantizedLinear
+    g = torch.Generator().manual_seed(0)
+    W = torch.randn(768, 768, generator=g) * 0.02
+    X = torch.randn(128, 512, 768, generator=g)
+    X[..., torch.randperm(768, generator=g)[:8]] *= 20
+    Wd, Xd = W.to(dev), X.to(dev)
+
+    def once(mode):
+        lin = torch.nn.Linear(768, 768).to(dev)
+        with torch.no_grad():
+            lin.weight.copy_(Wd)
+            lin.bias.zero_()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        q = GPTQ(lin, bits=4, group_size=128, blocksize=128, percdamp=0.01, device=dev)
+        for i in range(128):
+            q.add_batch(Xd[i:i + 1])
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        if mode == "reference":
+            q.quantize()
+        else:
+            q.fasterquant()
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        if mode == "reference":
+            q.pack_weights()
+        else:
+            QuantizedLinear.from_gptq(q)
+        torch.cuda.synchronize()
+        t3 = time.perf_counter()
+        return {"s": t3 - t0, "add_batch_s": t1 - t0, "quantize_s": t2 - t1, "pack_s": t3 - t2}
+
+    out = {}
+    for mode in ("reference", "canonical"):
+        once(mode)
+        runs = sorted((once(mode) for _ in range(reps)), key=lambda r: r["s"])
+        med = runs[len(runs) // 2]
+        out[mode] = {k: round(v, 5) for k, v in med.items()}
+    out["note"] = ("s per layer, add_batch x 128 to packed codes; median of 3 after one warm-up; "
+                   "reference = GPTQ.quantize + pack_weights, canonical = fasterquant + packed QuantizedLinear")
+    return out
+
+
 # ------------------------------------------------------------ CPU baseline --
 
 def _host_cpu():
@@ -417,49 +528,142 @@ def _host_cpu():
             "affinity_cores": len(os.sched_getaffinity(0))}
 
 
-def cpu_baseline(seconds_hint=20.0):
-    """The CPU oracle (numpy, this host's BLAS threads) on a bounded sample of
-    the block, extrapolated to one block the way the reference computes it:
-    one full-square fp32 Hessian per Linear over 128 x 2048 tokens, a fp32
-    Cholesky inverse per Linear, and the column sweep per Linear."""
+def _timed_cpu(fn, reps=1):
+    """Median wall time of ``reps`` calls (after one warm-up when reps > 1)."""
+    if reps > 1:
+        fn()
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return sorted(ts)[len(ts) // 2]
+
+
+BLOCK_LAYERS = [("q_proj", 4096, 4096), ("k_proj", 1024, 4096), ("v_proj", 1024, 4096), ("o_proj", 4096, 4096),
+                ("gate_proj", 14336, 4096), ("up_proj", 14336, 4096), ("down_proj", 4096, 14336)]
+
+
+def cpu_baseline():
+    """The CPU oracle (numpy, this host's BLAS threads) as the reference
+    computes, phase by phase (add_batch; damp + inverse; column sweep; pack):
+
+    * config 1 in full (768 x 768, 128 x 512 fp32 tokens), reference mode
+      (core/gptq.py:63-266 with the repair at :175) and canonical mode, one
+      warm-up then the median of 3;
+    * the config-3 block (128 x 2048 tokens), extrapolated per Linear from
+      measured samples: reference mode for the layers it defines (N <= K:
+      q/k/v/o/down), canonical mode for gate/up (N > K); one full-square
+      Hessian per Linear, as the reference accumulates it;
+    * config 4's fallback forward (models/layers.py:98-138, 155-157): the
+      fp32 dequantisation of the codes then F.linear in fp32, at the four
+      shapes and M = 1, 16, 128, measured in full."""
     import numpy as np
     from threadpoolctl import threadpool_info
     from oracle import gptq_oracle as O
     threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
     rng = np.random.default_rng(0)
+    t_all = time.perf_counter()
+
+    # -- config 1, in full
+    W1 = (rng.standard_normal((768, 768)) * 0.02).astype(np.float32)
+    X1 = rng.standard_normal((128, 512, 768), dtype=np.float32)
+    X1[..., rng.permutation(768)[:8]] *= 20
+    c1 = {}
+    for mode in ("reference", "canonical"):
+        ph = {}
+
+        def run(mode=mode, ph=ph):
+            t = time.perf_counter()
+            H, ns = None, 0
+            for i in range(128):
+                H, ns = O.add_batch(H, ns, X1[i:i + 1], dtype=np.float32)
+            t1 = time.perf_counter()
+            if mode == "reference":
+                Hinv = O.full_inverse(O.damp_ref(H, ns, 0.01))
+                t2 = time.perf_counter()
+                r = O.gptq_ref(W1, Hinv, 4, 128, 128)
+                t3 = time.perf_counter()
+                O.ref_pack_weights(r["codes"].astype(np.uint8), 4)
+            else:
+                Hc, dead = O.prepare_canonical_H(H, ns, 0.01)
+                U = O.upper_chol_of_inverse(Hc)
+                t2 = time.perf_counter()
+                r = O.gptq_canonical(W1, H, ns, 4, 128, 128, 0.01, dtype=np.float32, U=U)
+                t3 = time.perf_counter()
+                O.pack_bitstream(r["codes"].astype(np.uint8), 4)
+            t4 = time.perf_counter()
+            ph.setdefault("runs", []).append({"add_batch_s": t1 - t, "damp_inverse_s": t2 - t1, "sweep_s": t3 - t2,
+                                              "pack_s": t4 - t3, "s": t4 - t})
+        for _ in range(4):
+            run()
+        runs = sorted(ph["runs"][1:], key=lambda r: r["s"])
+        c1[mode] = {k: round(v, 4) for k, v in runs[1].items()}
+
+    # -- config 3, samples at K = 4096 (fp32)
     K = 4096
-    # (a) Hessian: 2 sequences of 2048 tokens at K = 4096, fp32
     x = rng.standard_normal((2, 2048, K), dtype=np.float32)
-    t = time.perf_counter()
-    O.add_batch(None, 0, x, dtype=np.float32)
-    t_h = (time.perf_counter() - t) / 2  # per sequence
-    # (b) damped inverse at K = 4096, fp32 (LAPACK)
-    H = (x.reshape(-1, K).T @ x.reshape(-1, K)).astype(np.float32) / 2
-    t = time.perf_counter()
-    O.upper_chol_of_inverse(O.damp_ref(H, 1, 0.01).astype(np.float32))
-    t_f = time.perf_counter() - t
-    # (c) sweep: canonical oracle on a 4096 x 1024 slice (fp32)
-    W = (rng.standard_normal((4096, 1024)) * 0.02).astype(np.float32)
-    Hs = H[:1024, :1024].astype(np.float32)
-    t = time.perf_counter()
-    O.gptq_canonical(W, Hs, 1, 4, 128, 128, 0.01, actorder=True, dtype=np.float32)
-    t_s = time.perf_counter() - t
-    sample = time.perf_counter()
-    layers = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336, 4096), (14336, 4096), (4096, 14336)]
-    hess = sum(128 * t_h * (k / K) ** 2 for _, k in layers)
-    fac = sum(t_f * (k / K) ** 3 for _, k in layers)
-    swp = sum(t_s * (n / 4096) * (k / 1024) ** 2 for n, k in layers)
-    total = hess + fac + swp
+    t_h = _timed_cpu(lambda: O.add_batch(None, 0, x, dtype=np.float32)) / 2          # per sequence
+    H = (x.reshape(-1, K).T @ x.reshape(-1, K)).astype(np.float32)
+    Hd = O.damp_ref(H, 2, 0.01).astype(np.float32)
+    t_inv = _timed_cpu(lambda: O.full_inverse(Hd))                                 # reference: full inverse
+    t_U = _timed_cpu(lambda: O.upper_chol_of_inverse(Hd))                          # canonical: upper factor
+    Hinv = O.full_inverse(Hd).astype(np.float32)
+    Wr = (rng.standard_normal((1024, K)) * 0.02).astype(np.float32)
+    t_rs = _timed_cpu(lambda: O.gptq_ref(Wr, Hinv, 4, 128, 128))                   # 1024 columns x K rows
+    Wc = (rng.standard_normal((4096, 1024)) * 0.02).astype(np.float32)
+    Hs = H[:1024, :1024].copy()
+    t_cs = _timed_cpu(lambda: O.gptq_canonical(Wc, Hs, 2, 4, 128, 128, 0.01, actorder=True, dtype=np.float32))
+    codes = rng.integers(0, 16, (4096, 4096)).astype(np.uint8)
+    t_rp = _timed_cpu(lambda: O.ref_pack_weights(codes, 4))
+    t_cp = _timed_cpu(lambda: O.pack_bitstream(codes, 4))
+    per_layer = {}
+    for name, N, Kl in BLOCK_LAYERS:
+        ref = N <= Kl
+        hs = 128 * t_h * (Kl / K) ** 2
+        inv = (t_inv if ref else t_U) * (Kl / K) ** 3
+        sw = t_rs * (N / 1024) * (Kl / K) if ref else t_cs * (N / 4096) * (Kl / 1024) ** 2
+        pk = (t_rp if ref else t_cp) * (N / 4096) * (Kl / 4096)
+        per_layer[name] = {"mode": "reference" if ref else "canonical", "add_batch_s": round(hs, 2),
+                           "damp_inverse_s": round(inv, 2), "sweep_s": round(sw, 2), "pack_s": round(pk, 3)}
+    phases = {k: round(sum(v[k] for v in per_layer.values()), 2)
+              for k in ("add_batch_s", "damp_inverse_s", "sweep_s", "pack_s")}
+    total = sum(phases.values())
+
+    # -- config 4's fallback forward, measured in full
+    c4 = {}
+    for (N, Kc) in GEMV_SHAPES:
+        q = rng.integers(0, 16, (N, Kc)).astype(np.uint8)
+        sc = rng.uniform(1e-3, 1e-2, (N, Kc // 128)).astype(np.float16)
+        zr = np.full((N, Kc // 128), 8.0, np.float16)
+        gi = np.arange(Kc) // 128
+        t = time.perf_counter()
+        Wd = O.dequant(q, sc, zr, gi)
+        t_un = time.perf_counter() - t
+        row = {"unpack_weights_s": round(t_un, 4)}
+        for M in (1, 16, 128):
+            xm = rng.standard_normal((M, Kc)).astype(np.float32)
+            row[f"linear_m{M}_s"] = round(_timed_cpu(lambda xm=xm, Wd=Wd: xm @ Wd.T, 3), 5)
+        c4[f"{N}x{Kc}"] = row
+        del Wd, q
+
     return {"value": round(total, 2), "unit": "s/block", "cores": threads, "kind": "port",
             "host": _host_cpu(),
-            "mode": "canonical GPTQ with act-order (the block's setting), oracle in fp32",
-            "sample": ("oracle/gptq_oracle.py in numpy fp32 on 2 x 2048 tokens (Hessian, K=4096), one damped "
-                       "Cholesky inverse at K=4096, one act-order sweep of 4096 x 1024; extrapolated per Linear "
-                       "of the block (Hessian x 128 sequences x (K/4096)^2, inverse x (K/4096)^3, sweep x "
-                       "N/4096 x (K/1024)^2) as the reference computes it (one full H per Linear)"),
-            "parts_s": {"hessian": round(hess, 2), "factor": round(fac, 2), "sweep": round(swp, 2)},
-            "sample_s": {"hessian_per_seq": round(t_h, 4), "factor_4096": round(t_f, 3),
-                         "sweep_4096x1024": round(t_s, 3)}}
+            "mode": ("reference mode (core/gptq.py semantics, repaired at :175) for q/k/v/o/down, canonical for "
+                     "gate/up (N > K, which the reference cannot run); oracle in numpy fp32"),
+            "sample": ("config 3 extrapolated per Linear from measured samples at K = 4096: add_batch of 2 x 2048 "
+                       "tokens (x 128 sequences x (K/4096)^2, one full-square H per Linear as the reference "
+                       "accumulates it), the damped full inverse / upper factor (x (K/4096)^3), the reference "
+                       "sweep of 1024 columns x 4096 rows (x N/1024 x K/4096) and the canonical act-order sweep "
+                       "of 4096 x 1024 (x N/4096 x (K/1024)^2), the 4096 x 4096 pack (x N K / 4096^2); config 1 "
+                       "and config 4's fallback forward measured in full"),
+            "measured": ["c1", "c4_fallback", "samples"], "extrapolated": ["value", "block_phases_s", "per_layer"],
+            "block_phases_s": phases, "per_layer": per_layer,
+            "samples_s": {"add_batch_per_seq_4096": round(t_h, 4), "full_inverse_4096": round(t_inv, 3),
+                          "upper_factor_4096": round(t_U, 3), "ref_sweep_1024x4096": round(t_rs, 3),
+                          "canonical_sweep_4096x1024": round(t_cs, 3), "ref_pack_4096x4096": round(t_rp, 4),
+                          "pack_4096x4096": round(t_cp, 4)},
+            "c1": c1, "c4_fallback": c4, "wall_s": round(time.perf_counter() - t_all, 1)}
 
 
 # ------------------------------------------------- kernel set for counters --
@@ -489,7 +693,21 @@ def run_kernels(args, torch, dev):
     src = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     out["copy_512MiB_ms"] = timed(lambda: dst.copy_(src), 3)
-    del src, dst
+    del dst
+    # the read-only launch at the largest W4A16 M = 1 byte count (28672 x 4096)
+    import ctypes
+
+    from distributed_gptq_amd import _lib
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    nb = gemv_bytes(28672, 4096, 4, 1)
+
+    def read():
+        st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        for r in range(8):
+            _lib.check(_lib.lib().gptq_stream_read(ctypes.c_void_p(src.data_ptr() + r * (64 << 20)), nb, 2048, 4,
+                                                   ctypes.c_void_p(flag.data_ptr()), st), "gptq_stream_read")
+    out["stream_read_62MB_us"] = round(timed(read, 3) * 1e3 / 8, 2)
+    del src
     g = torch.Generator(device=dev).manual_seed(5)
     n, K = args.nseq * args.seqlen, FFN
     X = torch.randn(n, K, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
@@ -568,29 +786,39 @@ def decoder_linears(model, torch):
 
 
 def run_model(args, torch, dev):
+    chosen = [r for r in MODELS[args.workload]["runs"] if not args.model_bits or r[0] in args.model_bits]
+    if not chosen:
+        raise SystemExit(f"--model-bits {args.model_bits}: no run of {args.workload} has those bits")
+    return _run_model(torch, dev, args.workload, chosen, args.warmup, args.true_sequential, args.model_nseq,
+                      args.model_chunk, args.seqlen)
+
+
+def _run_model(torch, dev, workload, chosen, warmup, true_sequential, nseq=0, chunk=0, seqlen=2048, base=None):
+    """Whole-model quantization (``DistributedGPTQuantizer.quantize_model``)
+    of the named shape for each (bits, group size, act-order) in ``chosen``,
+    each on a fresh copy of the model, after ``warmup`` untimed runs of the
+    first.  Returns the result dict and the base model (for reuse)."""
     import copy
 
     from distributed_gptq_amd import DistributedGPTQuantizer, QuantizationConfig
-    spec = MODELS[args.workload]
-    nseq = args.model_nseq or spec["nseq"]
-    log(f"[bench] {args.workload}: building the random-init model")
-    base = build_model(spec, torch, dev)
+    spec = MODELS[workload]
+    nseq = nseq or spec["nseq"]
+    if base is None:
+        log(f"[bench] {workload}: building the random-init model")
+        base = build_model(spec, torch, dev)
     names = decoder_linears(base, torch)
     g = torch.Generator(device=dev).manual_seed(spec["seed"])
-    ids = torch.randint(0, spec["vocab"], (nseq, args.seqlen), device=dev, generator=g)
-    chunk = args.model_chunk or spec["chunk"]
+    ids = torch.randint(0, spec["vocab"], (nseq, seqlen), device=dev, generator=g)
+    chunk = chunk or spec["chunk"]
     data = [ids[i:i + chunk] for i in range(0, nseq, chunk)]
     runs = []
     # untimed warm-up runs of the first setting (library initialisation, GEMM heuristics)
-    chosen = [r for r in spec["runs"] if not args.model_bits or r[0] in args.model_bits]
-    if not chosen:
-        raise SystemExit(f"--model-bits {args.model_bits}: no run of {args.workload} has those bits")
-    settings = [chosen[0]] * args.warmup + chosen
+    settings = [chosen[0]] * warmup + list(chosen)
     for idx, (bits, gs, actorder) in enumerate(settings):
-        timed = idx >= args.warmup
+        timed = idx >= warmup
         model = copy.deepcopy(base)
         cfg = QuantizationConfig(bits=bits, group_size=gs, actorder=actorder, calibration_samples=nseq,
-                                 true_sequential=args.true_sequential)
+                                 true_sequential=true_sequential)
         dq = DistributedGPTQuantizer(cfg)
         torch.cuda.synchronize()
         torch.cuda.reset_peak_memory_stats()
@@ -605,18 +833,37 @@ def run_model(args, torch, dev):
         wall = time.perf_counter() - t0
         free1, _ = torch.cuda.mem_get_info()
         errs = dq.quantization_errors
-        r = {"bits": bits, "group_size": gs, "actorder": actorder, "true_sequential": args.true_sequential,
+        r = {"bits": bits, "group_size": gs, "actorder": actorder, "true_sequential": true_sequential,
              "wall_s": round(wall, 3),
              "layers": len(errs), "peak_allocated_GiB": round(torch.cuda.max_memory_allocated() / 2**30, 2),
              "device_used_GiB_after": round((total - free1) / 2**30, 2),
              "total_error": float(sum(errs.values()))}
-        log(f"[bench] {args.workload} w{bits} g{gs}{'' if timed else ' (warm-up)'}: {r}")
+        log(f"[bench] {workload} w{bits} g{gs}{'' if timed else ' (warm-up)'}: {r}")
         if timed:
             runs.append(r)
         del model, dq
         torch.cuda.empty_cache()
     return {"runs": runs, "nseq": nseq, "layers": len(names), "chunk": chunk,
-            "params_GiB": round(sum(p.numel() for p in base.parameters()) * 2 / 2**30, 2)}
+            "params_GiB": round(sum(p.numel() for p in base.parameters()) * 2 / 2**30, 2)}, base
+
+
+def _c2(torch, dev):
+    """Config 2: the OPT-125m-shaped model, 4-bit g128, one warm-up run."""
+    m, _ = _run_model(torch, dev, "opt125m", MODELS["opt125m"]["runs"], 1, False)
+    return {"unit": "s/model", "workload": "opt125m", "nseq": m["nseq"], "quantized_linears": m["layers"],
+            **m["runs"][0]}
+
+
+def _c5(torch, dev):
+    """Config 5: the 13B-shaped model, 4-bit g128 act-order, one pass and
+    block by block (true-sequential), no warm-up run of its own (the block,
+    GEMV and config-2 runs before it have initialised the library)."""
+    m1, base = _run_model(torch, dev, "llama13b", [(4, 128, True)], 0, False)
+    m2, _ = _run_model(torch, dev, "llama13b", [(4, 128, True)], 0, True, base=base)
+    del base
+    return {"unit": "s/model", "workload": "llama13b", "nseq": m1["nseq"], "quantized_linears": m1["layers"],
+            "params_GiB": m1["params_GiB"], "one_pass": m1["runs"][0], "true_sequential": m2["runs"][0],
+            "other_settings": "2-bit g64 and 8-bit per-channel: bench.py --workload llama13b"}
 
 
 def main():
@@ -633,6 +880,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
     ap.add_argument("--no-block", action="store_true")
+    ap.add_argument("--no-models", action="store_true", help="skip configs 1, 2 and 5 in the default run")
     ap.add_argument("--no-3bit", action="store_true", help="skip the 3-bit block run")
     ap.add_argument("--workload", choices=["block", "kernels", *MODELS], default="block",
                     help="block: config 3 (default); opt125m: config 2; llama13b: config 5")
@@ -659,7 +907,7 @@ def main():
                           **run_kernels(args, torch, dev)}), flush=True)
         return
     if args.workload != "block":
-        m = run_model(args, torch, dev)
+        m, _ = run_model(args, torch, dev)
         spec = MODELS[args.workload]
         first = m["runs"][0]
         print(json.dumps({
@@ -740,6 +988,23 @@ def main():
         fu = run_fused(args, torch, dev)
         result["gemv"]["w4a16_m1_shared_input"] = fu
         log(f"[bench] W4A16 M=1 shared-input layers, separate vs one launch: {fu}")
+        # what one launch of the same bytes can read, and the GEMV against it
+        ceil = run_read_ceiling(torch, dev)
+        result["gemv"]["read_ceiling"] = ceil
+        result["gemv"]["w4a16_m1_frac_of_read_ceiling"] = {
+            k: round(ceil[k]["us"] / g4[k]["us"], 4) for k in ceil}
+        log(f"[bench] read-only launch at the W4A16 M=1 byte counts: {ceil}")
+    if not args.no_models:
+        # configs 1, 2 and 5 (each guarded: one failing run leaves the others' results)
+        for key, fn in (("c1", lambda: run_c1(torch, dev)), ("c2", lambda: _c2(torch, dev)),
+                        ("c5", lambda: _c5(torch, dev))):
+            try:
+                result[key] = fn()
+                log(f"[bench] {key}: {result[key]}")
+            except Exception as e:  # noqa: BLE001 -- recorded in the JSON line instead of losing it
+                result[key] = {"error": f"{type(e).__name__}: {e}"}
+                log(f"[bench] {key} failed: {e}")
+            torch.cuda.empty_cache()
     if args.no_block:
         result.setdefault("value", None)
     if not args.no_cpu:

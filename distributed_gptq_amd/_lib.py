@@ -64,6 +64,7 @@ SIGNATURES = {
                                       _p]),
     "gptq_quantize_tensor": (_i, [_p, _i, _i64, _i, _i, _i, _p, _p, _p, _p]),
     "gptq_dequantize_tensor": (_i, [_p, _i64, _i, _p, _p, _p, _p]),
+    "gptq_stream_read": (_i, [_p, _sz, _i, _i, _p, _p]),
 }
 
 

@@ -301,6 +301,18 @@ int gptq_dequantize_tensor(const int8_t* q, int64_t n, int group_size,
                            const float* scales, const float* zeros, float* out,
                            gptq_stream_t stream);
 
+/* ------------------------------------------------------- measurement aid --
+ * No counterpart in the reference: a read-only streaming kernel for the
+ * benchmark.  It reads `bytes` bytes of `buf` (both multiples of 16 bytes)
+ * with 16-byte non-temporal loads in a grid-stride loop of `blocks`
+ * workgroups of 256 threads, `unroll` (1, 2, 4 or 8) loads in flight per
+ * thread, and writes *flag = 1 only if a thread's XOR of its data equals a
+ * fixed value (so the reads are kept).  Timed at a GEMV's byte count it
+ * gives what one launch can read: the ceiling the M = 1 GEMV is compared
+ * with. */
+int gptq_stream_read(const void* buf, size_t bytes, int blocks, int unroll,
+                     uint32_t* flag, gptq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
