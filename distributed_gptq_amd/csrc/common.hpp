@@ -11,7 +11,7 @@
 #include <cstdio>
 #include <string>
 
-#include "../../include/gptq_hip.h"
+#include "plan.hpp"
 
 namespace gptq {
 
@@ -22,18 +22,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // -------------------------------------------------------------- errors ----
-void set_error(const char* fmt, ...);
-void clear_error();
-
+// (set_error, clear_error and GPTQ_REQUIRE come from status.hpp)
 inline hipStream_t as_hip(gptq_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
-
-#define GPTQ_REQUIRE(cond, code, ...)   \
-  do {                                  \
-    if (!(cond)) {                      \
-      ::gptq::set_error(__VA_ARGS__);   \
-      return (code);                    \
-    }                                   \
-  } while (0)
 
 // Checks the launch just enqueued.
 int check_launch(const char* what);
@@ -95,8 +85,7 @@ __device__ __forceinline__ void store_elem(void* p, int64_t i, int dtype, float 
   }
 }
 
-inline bool valid_dtype(int d) { return d == GPTQ_F32 || d == GPTQ_F16 || d == GPTQ_BF16; }
-inline int dtype_size(int d) { return d == GPTQ_F32 ? 4 : 2; }
+// (valid_dtype and dtype_size come from plan.hpp)
 __host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Orders one wave's LDS accesses for the compiler: lanes exchange data

@@ -431,19 +431,11 @@ struct Ctx {
   int32_t* info;
 };
 
-int64_t split_of(int64_t m) {
-  const int64_t nb = cdiv(m, kNB);
-  return ((nb + 1) / 2) * kNB;
-}
+static_assert(plan::kFactorLeaf == kNB, "the recursion's split rule and scratch size assume this leaf size");
 
-// scratch needed below a node of size m: 2 * m2 * m1 floats at this node +
-// whatever the right child needs (the left child's scratch is reused)
-int64_t scratch_floats(int64_t m) {
-  if (m <= kNB) return 0;
-  const int64_t m1 = split_of(m), m2 = m - m1;
-  return 2 * m2 * m1 + std::max(scratch_floats(m1), scratch_floats(m2));
-}
-
+// a node of size m splits into m1 = plan::factor_split(m) (whole leaves) and
+// m - m1; the scratch below it (plan::factor_scratch_floats) holds L21 and T2
+// of this node, then the right child's scratch
 int chol_inv(Ctx& c, int64_t n0, int64_t m, float* tmp) {
   const int64_t ld = c.K;
   if (m <= kNB) {
@@ -451,7 +443,7 @@ int chol_inv(Ctx& c, int64_t n0, int64_t m, float* tmp) {
                        static_cast<int>(m), c.info);
     return check_launch("chol_inv_leaf");
   }
-  const int64_t m1 = split_of(m), m2 = m - m1;
+  const int64_t m1 = plan::factor_split(m), m2 = m - m1;
   float* L21 = tmp;             // m2 x m1
   float* T2 = tmp + m2 * m1;    // m2 x m1
   float* deeper = tmp + 2 * m2 * m1;
@@ -482,16 +474,6 @@ int chol_inv(Ctx& c, int64_t n0, int64_t m, float* tmp) {
 }  // namespace gptq
 
 using namespace gptq;
-
-static size_t factor_ws_floats(int64_t K) {
-  // [lambda pad 64 floats][A K*K][scratch]
-  return 64 + static_cast<size_t>(K) * K + static_cast<size_t>(scratch_floats(K));
-}
-
-extern "C" size_t gptq_factor_workspace_size(int64_t K) {
-  if (K <= 0) return 0;
-  return factor_ws_floats(K) * sizeof(float);
-}
 
 extern "C" int gptq_damp_factor(const float* H, int64_t K, float scale, float percdamp, const int32_t* perm, int mode,
                                 float* Hd, float* out, int32_t* dead_cols, int32_t* info, void* workspace,

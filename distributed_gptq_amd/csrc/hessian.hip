@@ -674,36 +674,10 @@ __global__ __launch_bounds__(256) void hessian_reduce(float* __restrict__ H, int
   }
 }
 
-// Token splits.  Every split writes, and the reduce reads back, 512 KB per
-// tile, so splits cost traffic once they are short: at most 16384 tokens per
-// split (10240 for products of fewer than 512 tiles, K < 5888), and beyond
-// that only as many splits as bring the launch to ~512 workgroups while each
-// keeps >= 1024 tokens; at most 64.  Measured on MI355X (fp16 X): (n, K) =
-// (32768, 768) -> 32 splits, (32768, 3072) -> 7, (16384, 5120) -> 3,
-// (16384, 13824) -> 1, (262144, 14336) -> 16, each within 5% of the best split
-// count of a sweep over 1..64, and 1.2-1.5x faster than ~2048 workgroups for
-// the short calls; bf16 at (262144, 4096): 16 / 24 / 32 splits 4.57 / 4.47 /
-// 4.52 ms (26 now).
-int choose_splits(int64_t n, int ntiles) {
-  constexpr int64_t kTokMin = 1024, kMinWG = 512;
-  const int64_t tok_max = ntiles < 512 ? 10240 : 16384;
-  const int64_t fill = std::min<int64_t>(cdiv(kMinWG, static_cast<int64_t>(ntiles)), std::max<int64_t>(1, n / kTokMin));
-  const int64_t s = std::max<int64_t>(cdiv(n, tok_max), fill);
-  return static_cast<int>(std::min<int64_t>(std::max<int64_t>(s, 1), 64));
-}
-
 }  // namespace
 }  // namespace gptq
 
 using namespace gptq;
-
-extern "C" size_t gptq_hessian_workspace_size(int64_t n, int64_t K) {
-  if (n <= 0 || K <= 0) return 0;
-  const int64_t T = cdiv(K, kTile);
-  const int ntiles = static_cast<int>(T * (T + 1) / 2);
-  const int S = choose_splits(n, ntiles);
-  return static_cast<size_t>(S) * ntiles * kTile * kTile * sizeof(float);
-}
 
 namespace gptq {
 namespace {
@@ -748,12 +722,6 @@ int accumulate_run(float* H, const void* X, int64_t n, int64_t K, int64_t ldx, i
 }  // namespace
 }  // namespace gptq
 
-extern "C" size_t gptq_hessian_workspace_min(int64_t K) {
-  if (K <= 0) return 0;
-  const int64_t T = cdiv(K, kTile);
-  return static_cast<size_t>(T * (T + 1) / 2) * kTile * kTile * sizeof(float);
-}
-
 extern "C" int gptq_hessian_accumulate(float* H, const void* X, int64_t n, int64_t K, int64_t ldx, int dtype,
                                        void* workspace, size_t workspace_bytes, gptq_stream_t stream) {
   clear_error();
@@ -762,26 +730,24 @@ extern "C" int gptq_hessian_accumulate(float* H, const void* X, int64_t n, int64
                "hessian_accumulate: bad shape n=%lld K=%lld ldx=%lld", (long long)n, (long long)K, (long long)ldx);
   GPTQ_REQUIRE(valid_dtype(dtype), GPTQ_ERR_DTYPE, "hessian_accumulate: bad dtype %d", dtype);
   if (n == 0) return GPTQ_OK;
-  const int64_t T = cdiv(K, kTile);
-  const int ntiles = static_cast<int>(T * (T + 1) / 2);
-  const size_t split_bytes = static_cast<size_t>(ntiles) * kTile * kTile * sizeof(float);
+  const int ntiles = static_cast<int>(plan::hessian_tiles(K));
+  const size_t split_bytes = plan::hessian_split_bytes(K);
   GPTQ_REQUIRE(workspace && workspace_bytes >= split_bytes, GPTQ_ERR_WORKSPACE,
                "hessian_accumulate: workspace %zu < %zu bytes (one split's partial tiles)", workspace_bytes,
                split_bytes);
   float* part = static_cast<float*>(workspace);
   hipStream_t st = as_hip(stream);
-  const int S = choose_splits(n, ntiles);
+  const int S = plan::choose_splits(n, ntiles);
   if (static_cast<size_t>(S) * split_bytes <= workspace_bytes)
     return accumulate_run(H, X, n, K, ldx, dtype, S, part, st);
   // a smaller workspace: consecutive runs of tokens, each with as many splits
   // as the workspace holds, added to H one after the other (fixed order)
   const int64_t cap = static_cast<int64_t>(workspace_bytes / split_bytes);
-  int64_t run = cap * 16384;
-  while (run > 1024 && choose_splits(run, ntiles) > cap) run /= 2;
+  const int64_t run = plan::hessian_run_tokens(ntiles, cap);
   const int esz = dtype_size(dtype);
   for (int64_t t0 = 0; t0 < n; t0 += run) {
     const int64_t m = std::min<int64_t>(run, n - t0);
-    const int Sm = static_cast<int>(std::min<int64_t>(choose_splits(m, ntiles), cap));
+    const int Sm = static_cast<int>(std::min<int64_t>(plan::choose_splits(m, ntiles), cap));
     const int rc = accumulate_run(H, static_cast<const char*>(X) + t0 * ldx * esz, m, K, ldx, dtype, Sm, part, st);
     if (rc) return rc;
   }

@@ -1282,26 +1282,8 @@ int launch_reg4(hipStream_t st, const LinArgs& a, int splits = 1) {
   return check_launch("splitk_reduce");
 }
 
-// 1 < M <= 16 on layers of 4097-8191 rows: 32-row workgroups (160-255 of
-// them; 16-row ones would leave 64-127 CUs with two), and for K >= 8192 K
-// split in 3 when that keeps the grid within two workgroups per CU.
-// Measured on MI355X, 4-bit M = 16 (M = 8; M = 2): 5120 x 5120 12.9 (11.1;
-// 10.2) us against 16.0 (11.9; 11.6) with 16-row workgroups, 5120 x 13824
-// split 24.5 (21.2; 20.0) against 37.2 (27.2; 22.1), 6144 x 4096 11.0 (9.7;
-// 9.1) against 13.4 (10.2; 9.7).  Returns the split count, 0 outside these
-// shapes.
-inline int reg4_mid_splits(const LinArgs& a) {
-  if (!(a.M > 1 && a.M <= 16 && a.N > 4096 && a.N < 8192)) return 0;
-  return a.K >= 8192 && 3 * cdiv(a.N, 32) <= 512 && a.N % 4 == 0 ? 3 : 1;
-}
-
-// 1 < M <= 16 on 8192-row layers: 128 workgroups of 64 rows, so K split in
-// 2 (measured on MI355X, 4-bit 8192 x 8192, M = 16 / 4: 21.5 / 19.2 us
-// against 26.0 / 22.2 unsplit; on 11008-14336 rows, where the unsplit grid
-// is 172-224 workgroups, splitting measured 15-40% slower).  0 elsewhere.
-inline int reg4_wide_splits(const LinArgs& a) {
-  return a.M > 1 && a.M <= 16 && a.N >= 8192 && cdiv(a.N, 64) * 2 <= 256 && a.N % 4 == 0 && a.K >= 256 ? 2 : 0;
-}
+// (K splits of the register path on 4097-8192-row layers, 1 < M <= 16:
+// plan::reg4_mid_splits and plan::reg4_wide_splits)
 
 // Large products (M > 16 and enough output tiles): one workgroup per NT x MT
 // tile of (weight rows x activation rows), NT = 128 (K in steps of 64) or 64
@@ -1765,52 +1747,8 @@ int launch_rx(hipStream_t st, const LinArgs& a, int splits = 1) {
 // 170; 4096 x 14336 71 / 73 / 110 against 129 / 129 / 156; 28672 x 4096 123
 // / 128 / 176 against 174 / 178 / 257; 5120 x 13824 82 / 85 / 113 against
 // 125 / 151 / 156.
-struct RxPlan {
-  int splits = 0;
-  int waves = 8;
-  int rows = 16;  // weight rows per compute wave
-};
-
-inline RxPlan rx_plan(const LinArgs& a, int bits, bool rows32 = true) {
-  RxPlan p;
-  if (!((bits == 4 || bits == 3) && a.M > 16 && a.M <= 384 && (bits == 4 || a.pitch % 4 == 0))) return p;
-  if (a.M <= 32 && a.N * a.K <= (int64_t(1) << 24)) return p;
-  const int64_t mt = cdiv(a.M, 128);
-  const int64_t nblk = a.K / 128, cols8 = cdiv(a.N, 128) * mt, cols7 = cdiv(a.N, 112) * mt;
-  auto splits_for = [&](int64_t cols) {
-    int64_t sp = std::min<int64_t>(nblk, std::max<int64_t>(1, 256 / cols));
-    return cdiv(nblk, cdiv(nblk, sp));  // no empty split
-  };
-  int64_t grid = 0;
-  if (cols8 >= 192) {
-    p.splits = 1;
-    p.waves = cols7 <= 256 || cols8 > 256 ? 7 : 8;
-    grid = p.waves == 7 ? cols7 : cols8;
-  } else {
-    const int64_t s8 = splits_for(cols8), s7 = splits_for(cols7);
-    const bool w7 = cols7 * s7 > cols8 * s8;
-    const int64_t sp = w7 ? s7 : s8;
-    grid = w7 ? cols7 * s7 : cols8 * s8;
-    if ((sp > 1 && a.N % 4 != 0) || (sp == 1 && grid < 128)) return p;
-    p.splits = static_cast<int>(sp);
-    p.waves = w7 ? 7 : 8;
-  }
-  // 64 < M <= 128: 32 rows per compute wave (7 compute waves, 224 rows per
-  // workgroup) read each X fragment for two row blocks, where its grid is at
-  // least as large with at most 8 splits (measured, 4-bit M = 128, us: 28672 x
-  // 4096 68.3 -> 66.2, 14336 x 4096 44.0 -> 41.9, 13824 x 5120 50.1 -> 46.2,
-  // 22016 x 4096 63.2 -> 59.1, 11008 x 4096 40.7 -> 38.8; where its grid is
-  // smaller, slower: 16384 x 4096 47.5 -> 48.7, 8192 x 8192 49.6 -> 52.7)
-  if (rows32 && a.M > 64 && a.M <= 128) {
-    const int64_t cols32 = cdiv(a.N, 224), s32 = splits_for(cols32);
-    if (s32 <= 8 && cols32 * s32 >= grid && (s32 == 1 || a.N % 4 == 0)) {
-      p.splits = static_cast<int>(s32);
-      p.waves = 7;
-      p.rows = 32;
-    }
-  }
-  return p;
-}
+// (the plan itself, compute waves and K splits: plan::rx_plan)
+using plan::RxPlan;
 
 // the register-decoded kernel with W compute waves, activation tiles of 32,
 // 64 or 128 rows by M (M > 128: several tiles of 128)
@@ -1861,11 +1799,11 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
         return launch_reg4<BITS, 64, 4, BF16>(st, a);
       }
       if (a.N >= 32 * 256) {
-        const int s = reg4_wide_splits(a);
+        const int s = plan::reg4_wide_splits(a.M, a.N, a.K);
         const bool fits = s > 1 && a.part && static_cast<size_t>(s) * a.M * a.N * sizeof(float) <= a.part_bytes;
         return launch_reg4<BITS, 64, 8, BF16>(st, a, fits ? s : 1);
       }
-      if (const int s = reg4_mid_splits(a)) {
+      if (const int s = plan::reg4_mid_splits(a.M, a.N, a.K)) {
         const bool fits = a.part && static_cast<size_t>(s) * a.M * a.N * sizeof(float) <= a.part_bytes;
         return launch_reg4<BITS, 32, 8, BF16>(st, a, s > 1 && fits ? s : 1);
       }
@@ -1884,8 +1822,8 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
       return q.splits == 1 ||
              (q.splits > 1 && a.part && static_cast<size_t>(q.splits) * a.M * a.N * sizeof(float) <= a.part_bytes);
     };
-    RxPlan p = rx_plan(a, BITS);
-    if (p.rows == 32 && !fits(p)) p = rx_plan(a, BITS, false);  // no room for its partial sums
+    RxPlan p = plan::rx_plan(a.M, a.N, a.K, a.pitch, BITS);
+    if (p.rows == 32 && !fits(p)) p = plan::rx_plan(a.M, a.N, a.K, a.pitch, BITS, false);  // no room for its partial sums
     if (fits(p)) {
       // 32 rows per wave: 8 waves in all (one loader), so that each has 256
       // registers (with 10 waves it spilled), and two code slots
@@ -2063,19 +2001,7 @@ void launch_gather(hipStream_t st, const void* x, int esz, int64_t M, int64_t K,
   hipLaunchKernelGGL(gather_cols_k, grid, dim3(256), 0, st, x, esz, M, K, perm, out);
 }
 
-int check_linear_args(const void* x, int x_dtype, int64_t M, const uint8_t* packed, int bits, const void* scales,
-                      const void* zeros, int sz_dtype, const int32_t* g_idx, int group_size, int64_t ngroups,
-                      const void* bias, int bias_dtype, int64_t N, int64_t K, void* y) {
-  GPTQ_REQUIRE(x && packed && scales && zeros && y, GPTQ_ERR_ARG, "linear: null pointer");
-  GPTQ_REQUIRE(bits == 0 || bits == 2 || bits == 3 || bits == 4 || bits == 8, GPTQ_ERR_ARG, "linear: bits=%d", bits);
-  GPTQ_REQUIRE(valid_dtype(x_dtype) && valid_dtype(sz_dtype) && (!bias || valid_dtype(bias_dtype)), GPTQ_ERR_DTYPE,
-               "linear: bad dtype");
-  GPTQ_REQUIRE(M >= 0 && N > 0 && K > 0 && ngroups > 0 && (g_idx || group_size > 0), GPTQ_ERR_SHAPE,
-               "linear: bad shape");
-  GPTQ_REQUIRE(g_idx || cdiv(K, group_size) <= ngroups, GPTQ_ERR_SHAPE, "linear: too few groups");
-  GPTQ_REQUIRE(K <= INT32_MAX / 8, GPTQ_ERR_SHAPE, "linear: K=%lld too large", static_cast<long long>(K));
-  return GPTQ_OK;
-}
+using plan::check_linear_args;
 
 LinArgs make_linear_args(const void* x, int x_dtype, int64_t M, const uint8_t* packed, int bits, const void* scales,
                          const void* zeros, int sz_dtype, int group_size, int64_t ngroups, const void* bias,
@@ -2130,43 +2056,8 @@ extern "C" int gptq_linear(const void* x, int x_dtype, int64_t M, const uint8_t*
   return dispatch_linear(as_hip(stream), a, bits, g_idx);
 }
 
-extern "C" size_t gptq_linear_perm_workspace_size(int64_t M, int64_t K, int x_dtype) {
-  if (M <= 0 || K <= 0 || !valid_dtype(x_dtype)) return 0;
-  return static_cast<size_t>(M) * static_cast<size_t>(K) * static_cast<size_t>(dtype_size(x_dtype));
-}
-
-namespace gptq {
-namespace {
-
-size_t round256(size_t b) { return (b + 255) / 256 * 256; }
-
-// split-K partial-sum bytes the register-decoded kernel would use for this
-// layer (0 when it does not split)
-size_t splitk_bytes(int64_t M, int64_t N, int64_t K, int bits, int group_size, int x_dtype) {
-  if (M <= 0 || N <= 0 || K <= 0 || x_dtype == GPTQ_F32 || K % 128 != 0 || group_size <= 0 || group_size % 32 != 0)
-    return 0;
-  LinArgs a{};
-  a.M = M;
-  a.N = N;
-  a.K = K;
-  a.pitch = (K * bits + 7) / 8;
-  // M <= 16: the register path stages <= 128 groups per row
-  const int sp = M > 16 ? rx_plan(a, bits).splits
-                        : (bits == 4 || bits == 3) && cdiv(K, group_size) <= 128
-                              ? std::max(reg4_mid_splits(a), reg4_wide_splits(a))
-                              : 0;
-  return sp > 1 ? static_cast<size_t>(sp) * M * N * sizeof(float) : 0;
-}
-
-}  // namespace
-}  // namespace gptq
-
-extern "C" size_t gptq_linear_workspace_size(int64_t M, int64_t N, int64_t K, int bits, int group_size, int x_dtype,
-                                             int has_perm) {
-  if (M <= 0 || N <= 0 || K <= 0 || !valid_dtype(x_dtype)) return 0;
-  const size_t gather = has_perm ? round256(static_cast<size_t>(M) * K * dtype_size(x_dtype)) : 0;
-  return gather + splitk_bytes(M, N, K, bits, group_size, x_dtype);
-}
+// (gptq_linear_perm_workspace_size and gptq_linear_workspace_size, with the
+// split-K partial-sum bytes, are in plan.cpp)
 
 extern "C" int gptq_linear_ws(const void* x, int x_dtype, int64_t M, const int32_t* perm, const uint8_t* packed,
                               int bits, const void* scales, const void* zeros, int sz_dtype, const int32_t* g_idx,
@@ -2188,7 +2079,7 @@ extern "C" int gptq_linear_ws(const void* x, int x_dtype, int64_t M, const int32
     const int lrc = check_launch("gather_cols");
     if (lrc != GPTQ_OK) return lrc;
     a.x = static_cast<const uint16_t*>(workspace);
-    used = round256(need);
+    used = plan::round256(need);
   }
   // the rest of the workspace, from its first 256-byte boundary, holds
   // split-K partial sums when the kernel takes them and they fit (else the

@@ -573,18 +573,12 @@ int launch_r16(hipStream_t st, const SubArgs& a) {
 using namespace gptq;
 
 // Trailing updates are batched two-level: each sub-block updates the rest of
-// its run of blocks spanning >= kRun columns right away (the columns swept
+// its run of blocks spanning >= plan::kSweepRun columns right away (the columns swept
 // next), and the run's errors update everything after it in one GEMM of
-// depth >= kRun at the run's end.  Errors of a run are kept side by side.
-constexpr int64_t kRun = 512;
-
-int64_t run_blocks(int blocksize) { return std::max<int64_t>(1, cdiv(kRun, blocksize)); }
-
-extern "C" size_t gptq_sweep_workspace_size(int64_t rows, int64_t cols, int blocksize) {
-  (void)cols;
-  if (rows <= 0 || blocksize <= 0) return 0;
-  return static_cast<size_t>(rows) * std::max<int64_t>(kSub, run_blocks(blocksize) * blocksize) * sizeof(float);
-}
+// depth >= plan::kSweepRun at the run's end.  Errors of a run are kept side by side.
+// (plan::kSweepRun = 512 columns, plan::sweep_run_blocks; the workspace
+// size is gptq_sweep_workspace_size in plan.cpp)
+static_assert(plan::kSweepSub == kSub, "the sweep workspace size assumes this sub-block width");
 
 extern "C" int gptq_minmax_params(const float* src, int64_t rows, int64_t cols, int64_t ld, int bits, int group_size,
                                   int flags, float* scale, float* zero, gptq_stream_t stream) {
@@ -683,7 +677,7 @@ extern "C" int gptq_quantize_sweep(float* W, const float* W0, const float* T, in
   // writes from every sub-block would each touch their own cache line).
   const bool defer = out_cols != nullptr && cols <= kUnpermMaxCols;
   // without the trailing update every block stands alone (one Err slot)
-  const int64_t F = trailing ? run_blocks(blocksize) : 1;
+  const int64_t F = trailing ? plan::sweep_run_blocks(blocksize) : 1;
   const int64_t lde = trailing ? std::max<int64_t>(kSub, F * blocksize) : kSub;
   for (int64_t s1 = 0; s1 < cols; s1 += F * blocksize) {
     const int64_t s2 = std::min<int64_t>(s1 + F * blocksize, cols);
