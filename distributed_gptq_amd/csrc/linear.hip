@@ -600,15 +600,19 @@ __global__ __launch_bounds__(256) void gemv_m1_k(LinArgs a) {
       }
     }
   };
+  // the next batch is prefetched only where there is one: a prefetch past
+  // the last batch (empty descriptors, no memory traffic) still cost 3-10%
+  // of the launch (measured on MI355X over the four config-4 shapes, 4- and
+  // 3-bit, e.g. 3-bit 14336 x 4096 9.9 -> 8.9 us)
   for (;;) {
     float acc[RB], bias;
-    load_m1_batch<BITS, MAXC, RB>(a, (rb + step) * RB, coff, goff, B);
+    if (rb + step < nbatches) load_m1_batch<BITS, MAXC, RB>(a, (rb + step) * RB, coff, goff, B);
     __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
     m1_rows<BITS, BF16, SZBF, MAXC, RB>(A, xr, xsr, ysr, magic, bias_bf, acc, bias);
     finish(acc, bias, rb * RB);
     rb += step;
     if (rb >= nbatches) break;
-    load_m1_batch<BITS, MAXC, RB>(a, (rb + step) * RB, coff, goff, A);
+    if (rb + step < nbatches) load_m1_batch<BITS, MAXC, RB>(a, (rb + step) * RB, coff, goff, A);
     __builtin_amdgcn_sched_barrier(0);
     m1_rows<BITS, BF16, SZBF, MAXC, RB>(B, xr, xsr, ysr, magic, bias_bf, acc, bias);
     finish(acc, bias, rb * RB);
