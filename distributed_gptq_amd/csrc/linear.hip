@@ -1200,12 +1200,52 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
   if (b + WAVES < nblk) load(b + WAVES, B);
 
   // the workgroup's scales and zeros (contiguous rows of the [N][ngroups]
-  // arrays) are staged once with coalesced loads: per block a lane then reads
-  // its pairs from LDS instead of 16-row gathers
-  for (int e = tid; e < NT * ng; e += 64 * WAVES) {
-    const int64_t n = std::min<int64_t>(n0 + e / ng, a.N - 1);
-    const int64_t off = n * a.ngroups + e % ng;
-    sz[(e % ng) * NT + e / ng] = float2{load_elem(a.scales, off, a.sz_dtype), load_elem(a.zeros, off, a.sz_dtype)};
+  // arrays) are staged once in LDS: per block a lane then reads its pairs
+  // from LDS instead of 16-row gathers.  Element e = r ng + g of the rows'
+  // chunk goes to sz[g][r].  Where both chunks are 16-byte aligned a lane
+  // loads 16 bytes of each per round (8 halves or 4 floats; rows past N read
+  // as zeros through the buffer descriptors) and steps (r, g) along them:
+  // one round for up to 4096 halves per array, where one element pair per
+  // lane and round made the staging a chain of memory round trips
+  {
+    constexpr int kPer = 64 * WAVES;
+    const int tot = NT * ng;
+    const int esz = a.sz_dtype == GPTQ_F32 ? 4 : 2;
+    const char* sb = static_cast<const char*>(a.scales) + n0 * a.ngroups * esz;
+    const char* zb = static_cast<const char*>(a.zeros) + n0 * a.ngroups * esz;
+    if (((reinterpret_cast<uintptr_t>(sb) | reinterpret_cast<uintptr_t>(zb)) & 15u) == 0) {
+      const uint32_t bytes = static_cast<uint32_t>(std::min<int64_t>(NT, a.N - n0) * ng * esz);
+      const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb, bytes), zrs = make_rsrc(zb, bytes);
+      const int epv = 16 / esz;
+      const int nvec = static_cast<int>(cdiv(tot, epv));
+      for (int v = tid; v - lane < nvec; v += kPer) {
+        const uint32_t off = 16u * static_cast<uint32_t>(v);
+        const u32x4 sv = __builtin_amdgcn_raw_buffer_load_b128(srs, off, 0, 0);
+        const u32x4 zv = __builtin_amdgcn_raw_buffer_load_b128(zrs, off, 0, 0);
+        const int e0 = v * epv;
+        if (e0 >= tot) continue;
+        int r = e0 / ng, g = e0 - r * ng;
+        auto put = [&](float sv_, float zv_) {
+          if (r < NT) sz[g * NT + r] = float2{sv_, zv_};
+          if (++g == ng) { g = 0; ++r; }
+        };
+        if (esz == 4) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) put(__builtin_bit_cast(float, sv[j]), __builtin_bit_cast(float, zv[j]));
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            put(elem_value((sv[j / 2] >> (16 * (j & 1))) & 0xFFFFu, false, a.sz_dtype),
+                elem_value((zv[j / 2] >> (16 * (j & 1))) & 0xFFFFu, false, a.sz_dtype));
+        }
+      }
+    } else {
+      for (int e = tid; e < tot; e += kPer) {
+        const int64_t off = std::min<int64_t>(n0 + e / ng, a.N - 1) * a.ngroups + e % ng;
+        sz[(e % ng) * NT + e / ng] =
+            float2{load_elem(a.scales, off, a.sz_dtype), load_elem(a.zeros, off, a.sz_dtype)};
+      }
+    }
   }
   __syncthreads();
 
@@ -1572,17 +1612,31 @@ __global__ __launch_bounds__(64 * (WAVES + L)) __attribute__((amdgpu_waves_per_e
                                                     0, 0);
   };
   // GPTQ zero points are integers: with fp16 activations, fp16 scales (exact
-  // in the packed multiply, so (q - z) * s rounds once) and every zero of the
-  // wave's rows an integer in [0, 1023] the decode is packed fp16 math
-  // ((1024 + q) - (1024 + z) exact, then * s), decided once
+  // in the packed multiply, so (q - z) * s rounds once) and every zero the
+  // wave uses (its rows, the groups of this workgroup's columns) an integer
+  // in [0, 1023] the decode is packed fp16 math ((1024 + q) - (1024 + z)
+  // exact, then * s), decided once.  Eight loads per lane are in flight: one
+  // dependent load per group made the check a chain of memory round trips
+  // ahead of the first block
   bool pk = !BF16 && a.sz_dtype == GPTQ_F16;
   if constexpr (!BF16) {
-    for (int64_t g = g4; g < a.ngroups; g += 4)
+    if (pk) {
+      const int64_t g_lo = static_cast<int64_t>(kb0) * 128 / a.gs;
+      const int64_t g_hi = std::min<int64_t>(a.ngroups, (static_cast<int64_t>(kb0 + nblk) * 128 - 1) / a.gs + 1);
+      for (int64_t g0 = g_lo + g4; g0 < g_hi; g0 += 32) {
+        float z[8][NB];
 #pragma unroll
-      for (int i = 0; i < NB; ++i) {
-        const float z = load_elem(a.zeros, wn[i] * a.ngroups + g, a.sz_dtype);
-        pk = pk && z == rintf(z) && z >= 0.0f && z <= 1023.0f;
+        for (int u = 0; u < 8; ++u) {
+          const int64_t g = std::min<int64_t>(g0 + 4 * u, g_hi - 1);
+#pragma unroll
+          for (int i = 0; i < NB; ++i) z[u][i] = load_elem(a.zeros, wn[i] * a.ngroups + g, a.sz_dtype);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+          for (int i = 0; i < NB; ++i) pk = pk && z[u][i] == rintf(z[u][i]) && z[u][i] >= 0.0f && z[u][i] <= 1023.0f;
       }
+    }
     pk = __all(pk);
   }
 
