@@ -1517,13 +1517,13 @@ struct RxCodes {
   bool sh[NW / 16], zh[NW / 16];
 };
 
-template <int BITS, bool BF16, int NW, int WAVES, int L, int MT, int S, int OCC>
+template <int BITS, bool BF16, int NW, int WAVES, int L, int MT, int S, int OCC, int XD>
 __global__ __launch_bounds__(64 * (WAVES + L)) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void dq_rx_k(LinArgs a) {
   static_assert(BITS == 4 || BITS == 3, "4- or 3-bit codes");
   constexpr int NB = NW / 16, MB = MT / 16;
   constexpr int P = 128 + 8;              // LDS row pitch (halves)
   constexpr int XP = MT * 16 / (64 * L);  // 16-byte X pieces per loader lane and block
-  static_assert(NW % 16 == 0 && MT % 16 == 0 && (MT * 16) % (64 * L) == 0 && S >= 2, "tile shape");
+  static_assert(NW % 16 == 0 && MT % 16 == 0 && (MT * 16) % (64 * L) == 0 && S >= 2 && S % 2 == 0, "tile shape");
   __shared__ __attribute__((aligned(16))) uint16_t sX[2][MT * P];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1544,31 +1544,54 @@ __global__ __launch_bounds__(64 * (WAVES + L)) __attribute__((amdgpu_waves_per_e
     const int64_t rows = std::min<int64_t>(MT, a.M - m0);
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x + m0 * a.K, static_cast<uint32_t>(rows * a.K * 2));
     const uint32_t voff = static_cast<uint32_t>((e0 / 16) * a.K * 2 + 16 * (e0 % 16));
-    uint4 xr[XP];
-    auto load_x = [&](int b) {
+    // XD register sets: block b is loaded into set b % XD, XD blocks before
+    // it is stored.  With one set the loop waits a full memory round trip per
+    // block; two give a load two blocks' time to arrive, where the compute
+    // waves leave the registers for them.  The loads are unconditional (past
+    // the last block they repeat it), so every path issues the same loads
+    // and each wait is for the oldest set only
+    uint4 xr[XD][XP];
+    auto load_x = [&](int b, int set) {
+      b = std::min(b, nblk - 1);
 #pragma unroll
       for (int v = 0; v < XP; ++v) {
         const uint32_t off = static_cast<uint32_t>((4 * L * v * a.K + static_cast<int64_t>(kb0 + b) * 128) * 2);
-        xr[v] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, voff + off, 0, 0));
+        xr[set][v] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, voff + off, 0, 0));
       }
     };
-    auto store_x = [&](int buf) {
+    auto store_x = [&](int buf, int set) {
 #pragma unroll
       for (int v = 0; v < XP; ++v) {
         const int e = e0 + 64 * L * v;
-        *reinterpret_cast<uint4*>(&sX[buf][(e / 16) * P + 8 * (e % 16)]) = perm_0415(xr[v]);
+        *reinterpret_cast<uint4*>(&sX[buf][(e / 16) * P + 8 * (e % 16)]) = perm_0415(xr[set][v]);
       }
     };
-    load_x(0);
-    store_x(0);
-    if (nblk > 1) load_x(1);
-    __syncthreads();
-    for (int j = 0; j < nsteps; ++j) {
-      if (j + 1 < nblk) {
-        store_x((j + 1) & 1);
-        if (j + 2 < nblk) load_x(j + 2);
-      }
+    if constexpr (XD == 1) {
+      load_x(0, 0);
+      store_x(0, 0);
+      load_x(1, 0);
       __syncthreads();
+      for (int j = 0; j < nsteps; ++j) {
+        if (j + 1 < nblk) store_x((j + 1) & 1, 0);
+        load_x(j + 2, 0);
+        __syncthreads();
+      }
+    } else {
+      load_x(0, 0);
+      load_x(1, 1);
+      store_x(0, 0);
+      load_x(2, 0);
+      __syncthreads();
+      // steps in pairs, so that each set index is a constant (nsteps is a
+      // multiple of S, which is even)
+      for (int j = 0; j < nsteps; j += 2) {
+        if (j + 1 < nblk) store_x(1, 1);
+        load_x(j + 3, 1);
+        __syncthreads();
+        if (j + 2 < nblk) store_x(0, 0);
+        load_x(j + 4, 0);
+        __syncthreads();
+      }
     }
     return;
   }
@@ -1769,11 +1792,11 @@ __global__ __launch_bounds__(64 * (WAVES + L)) __attribute__((amdgpu_waves_per_e
   }
 }
 
-template <int BITS, bool BF16, int NW, int WAVES, int L, int MT, int S, int OCC>
+template <int BITS, bool BF16, int NW, int WAVES, int L, int MT, int S, int OCC, int XD>
 int launch_rx(hipStream_t st, const LinArgs& a, int splits = 1) {
   const dim3 grid(static_cast<unsigned>(cdiv(a.N, NW * WAVES)), static_cast<unsigned>(cdiv(a.M, MT)),
                   static_cast<unsigned>(splits));
-  hipLaunchKernelGGL((dq_rx_k<BITS, BF16, NW, WAVES, L, MT, S, OCC>), grid, dim3(64 * (WAVES + L)), 0, st, a);
+  hipLaunchKernelGGL((dq_rx_k<BITS, BF16, NW, WAVES, L, MT, S, OCC, XD>), grid, dim3(64 * (WAVES + L)), 0, st, a);
   int rc = check_launch("dq_rx");
   if (rc != GPTQ_OK || splits == 1) return rc;
   const int64_t quads = a.M * a.N / 4;
@@ -1812,9 +1835,9 @@ using plan::RxPlan;
 // 64 or 128 rows by M (M > 128: several tiles of 128)
 template <int BITS, bool BF16, int W>
 int launch_rx_w(hipStream_t st, const LinArgs& a, int splits) {
-  if (a.M <= 32) return launch_rx<BITS, BF16, 16, W, 1, 32, 4, 2>(st, a, splits);
-  if (a.M <= 64) return launch_rx<BITS, BF16, 16, W, 2, 64, 4, 2>(st, a, splits);
-  return launch_rx<BITS, BF16, 16, W, 2, 128, 4, 2>(st, a, splits);
+  if (a.M <= 32) return launch_rx<BITS, BF16, 16, W, 1, 32, 4, 2, 2>(st, a, splits);
+  if (a.M <= 64) return launch_rx<BITS, BF16, 16, W, 2, 64, 4, 2, 2>(st, a, splits);
+  return launch_rx<BITS, BF16, 16, W, 2, 128, 4, 2, 2>(st, a, splits);
 }
 
 template <int BITS, bool BF16, int NT, int MT, int WAVES>
@@ -1883,9 +1906,10 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
     RxPlan p = plan::rx_plan(a.M, a.N, a.K, a.pitch, BITS);
     if (p.rows == 32 && !fits(p)) p = plan::rx_plan(a.M, a.N, a.K, a.pitch, BITS, false);  // no room for its partial sums
     if (fits(p)) {
-      // 32 rows per wave: 8 waves in all (one loader), so that each has 256
-      // registers (with 10 waves it spilled), and two code slots
-      if (p.rows == 32) return launch_rx<BITS, BF16, 32, 7, 1, 128, 2, 2>(st, a, p.splits);
+      // 32 rows per wave: 8 waves in all (one loader with one register set),
+      // so that each has 256 registers (with 10 waves, or 9 with two loader
+      // sets, they spilled), and two code slots
+      if (p.rows == 32) return launch_rx<BITS, BF16, 32, 7, 1, 128, 2, 2, 1>(st, a, p.splits);
       return p.waves == 7 ? launch_rx_w<BITS, BF16, 7>(st, a, p.splits) : launch_rx_w<BITS, BF16, 8>(st, a, p.splits);
     }
   }
