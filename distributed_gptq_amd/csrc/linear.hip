@@ -1536,6 +1536,12 @@ __global__ __launch_bounds__(64 * (WAVES + L)) __attribute__((amdgpu_waves_per_e
   const int nsteps = static_cast<int>(cdiv(nblk, S)) * S;  // whole rounds of the S code slots
 
   if (wave >= WAVES) {
+    // the loaders' LDS stores compete with the compute waves' fragment
+    // reads; at the default priority they waited behind them and the
+    // barrier held the compute waves (per-wave timestamps at 4096 x 14336,
+    // M = 128: stores 3200 -> 1000 cycles a block, compute waves' barrier
+    // wait 1550 -> 920 cycles)
+    __builtin_amdgcn_s_setprio(3);
     // loaders: piece e = 64 (wave - WAVES) + 64 L v + lane is row e / 16,
     // columns 8 (e % 16) .. + 7 of the block, read through a buffer descriptor
     // that ends at the last row of X (rows past M read as zeros, with no
