@@ -272,9 +272,10 @@ __device__ __forceinline__ void gemm_tile(const GemmDesc& d, int bid, float* __r
 // fp32 MFMA kernels: the K = 14336 damped factorisation 29.0 -> 20.9 ms and
 // the 4096 x 14336 column sweep 10.8 -> 8.0 ms; the factor's residual
 // |U Hd U^T - I|_F / sqrt(K) 1.6e-6 -> 1.9e-6 (its distance to the fp64
-// factor 1.0e-6 -> 1.5e-6).  Tried and slower: two LDS stage buffers with
-// the split interleaved under the MFMAs, one workgroup per CU (21.9 ms);
-// prefetching two stages ahead (no change).
+// factor 1.0e-6 -> 1.5e-6).  Loads run two stages ahead (in two register
+// sets; one stage ahead measured the same).  Tried and not kept: two LDS
+// stage buffers with the split interleaved under the MFMAs, one workgroup
+// per CU (21.9 ms); a start offset for every second workgroup (no change).
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float fl2 __attribute__((ext_vector_type(2)));
@@ -390,8 +391,6 @@ struct alignas(16) X3Smem {
   X3Planes<TN, BK> b;
 };
 
-// output tile `bid` of d on the split-bf16 MFMAs (A [i][k] with 16-byte
-// rows, as kVec; B as kTB)
 // C tile (i0, j0) of d from the waves' 32x32 accumulators (the fp32
 // kernel's epilogue)
 template <int FM, int FN>
@@ -429,6 +428,8 @@ __device__ __forceinline__ void x3_epilogue(const GemmDesc& d, int64_t i0, int64
     }
 }
 
+// output tile `bid` of d on the split-bf16 MFMAs (A [i][k] with 16-byte
+// rows, as kVec; B as kTB)
 template <int TM, int TN, int BK, bool kTB>
 __device__ __forceinline__ void gemm_tile_x3(const GemmDesc& d, int bid, X3Smem<TM, TN, BK>& sm) {
   constexpr int FM = TM / 64, FN = TN / 64;  // 32x32 blocks per wave
@@ -464,8 +465,7 @@ __device__ __forceinline__ void gemm_tile_x3(const GemmDesc& d, int bid, X3Smem<
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
   // two register sets: stage s is loaded into set s % 2 two stages before
-  // it is stored, so a load has two stages of MFMAs to arrive (the MFMAs of
-  // one stage are too short to hide a memory round trip)
+  // it is stored
   f32x4 pa[2][QA], pb[2][QB];
   uint32_t oka[2] = {0, 0}, okb[2] = {0, 0};
   // a stage inside both operands (every stage of an interior tile) skips
