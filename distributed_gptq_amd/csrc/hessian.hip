@@ -288,8 +288,8 @@ void hessian_tile16(const uint16_t* __restrict__ X, int64_t n, int K, int64_t ld
 }
 
 // ------------------------------------------- 16-bit inputs, LDS DMA path ----
-// For 16-byte aligned rows.  Per stage of 64 tokens, each operand's slab
-// (64 tokens x 256 features, token-major, 32 KB) is copied into LDS by
+// For 16-byte aligned rows.  Per stage of 48 tokens, each operand's slab
+// (48 tokens x 256 features, token-major, 24 KB) is copied into LDS by
 // buffer_load_dwordx4 ... lds (one instruction = 1 KB = 2 token rows; tokens
 // past the split and features past K read as zeros) -- no registers, no
 // transposes.  MFMA fragments (8 consecutive tokens of one feature per lane)
@@ -297,11 +297,35 @@ void hessian_tile16(const uint16_t* __restrict__ X, int64_t n, int K, int64_t ld
 // addresses token r, features 4q..4q+3 of a 4 x 16 block and lane i receives
 // feature i of the 4 tokens.  The 16-byte slots of token row t are XOR-
 // swizzled by dma_sig(t & 3) so that these reads hit distinct banks whether an
-// LDS pass serves 16 or 32 lanes.  Waves form a (256 / WM) x (256 / WN) grid of
-// WM x WN blocks; one barrier per stage, the next stage's copy is in flight
-// during the current stage's MFMAs.
-constexpr int kRowB = 512;          // one token row of a slab
-constexpr int kSlabB = 64 * kRowB;  // one operand, one stage
+// LDS pass serves 16 or 32 lanes.
+//
+// One workgroup of 4 waves (one per SIMD) per (split, tile); wave w owns the
+// 128 x 128 block (w / 2, w % 2) of the 256 x 256 tile as 4 x 4 MFMA 32x32
+// blocks, 256 fp32 accumulators per lane in AGPRs.  Per 16 tokens (a step) a
+// wave reads 8 fragments (16 LDS reads) for 16 MFMAs.
+//
+// Schedule, per stage of three steps out of one of three LDS buffers:
+//   * fragments are read one step ahead into three register sets (step q of
+//     a stage uses set q), two LDS reads after each of a step's first 8 MFMAs;
+//   * the stage barrier sits after the first 8 MFMAs of the last step: before
+//     it a wave waits for its own copies of the next stage (those of the
+//     stage after it stay in flight) and for its LDS reads of this stage;
+//     after it the next stage's first fragments are read under the step's
+//     last 8 MFMAs.  The barrier is a bare s_barrier: these waits are all it
+//     needs, and the compiler's full wait before a barrier would also wait
+//     for the copies still in flight;
+//   * each wave issues 12 copies per stage, one after every fourth MFMA of
+//     the first two steps (4 + 4 copies of the stage two ahead, into the
+//     buffer freed at the previous stage's barrier) and after every second
+//     MFMA of the last step's tail (4 copies of the stage three ahead, into
+//     this stage's buffer).  Spread this way the copies cost 8-9% less time
+//     than issued together after the barrier.
+//   * the MFMAs are inline asm (accumulators pinned to AGPRs, fragments to
+//     VGPRs; with the builtin the register allocator moved accumulators
+//     through VGPRs and spilled).  volatile keeps them in program order with
+//     the LDS reads and copies; the compiler still places the LDS waits
+//     before each MFMA from its operands.
+constexpr int kRowB = 512;  // one token row of a slab
 
 __device__ __forceinline__ int dma_sig(int r) { return 10 * (r & 1) + 4 * ((r >> 1) & 1); }
 
@@ -317,11 +341,10 @@ __device__ __forceinline__ u32x4 tr_frag(const uint8_t* p) {
   return u32x4{a.x, a.y, b.x, b.y};
 }
 
-// Stages of kDmaBK = 48 tokens rotate through three buffers (144 KB): the
-// copies of two stages are in flight while a third is multiplied out.  The
-// buffers are distinct LDS variables and the stage loop is unrolled by three,
-// so the compiler can tell the buffers being copied into from the one being
-// read and does not wait for the copies before the reads.
+// Three stage buffers (3 x 48 KB).  They are distinct LDS variables selected
+// at compile time (the stage loop is unrolled by three), so the compiler can
+// tell the buffers being copied into from the one being read and does not
+// wait for the copies before the reads.
 constexpr int kDmaBK = 48;
 constexpr int kStageB = kDmaBK * kRowB;  // one operand, one stage
 __shared__ __attribute__((aligned(1024))) uint8_t g_hslab0[2][kStageB];
@@ -333,155 +356,244 @@ __device__ __forceinline__ uint8_t* hslab(int op) {
   return B == 0 ? &g_hslab0[op][0] : B == 1 ? &g_hslab1[op][0] : &g_hslab2[op][0];
 }
 
-// s_waitcnt for "at most N vector-memory operations outstanding" (gfx9
-// encoding: vmcnt low bits 3:0, expcnt 6:4 and lgkmcnt 11:8 left at "no wait")
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N < 16, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+template <int I, int N, class F>
+__device__ __forceinline__ void sfor(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    sfor<I + 1, N>(f);
+  }
 }
 
-template <bool kBF16, int WM, int WN, int kMap = 0>
-__global__ __launch_bounds__((256 / WM) * (256 / WN) * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
-void hessian_dma16(const uint16_t* __restrict__ X, int64_t n, int K, int64_t ldx, int S, int64_t tok_per_split,
-                   int ntiles, float* __restrict__ partial) {
-  // 128 x 128 blocks keep their 256 accumulators per lane in AGPRs: an AGPR
-  // clobber makes the compiler select the AGPR form of the MFMAs
-  if constexpr (WM * WN > 128 * 64) asm volatile("" ::: "a0");
-  constexpr int kW = (256 / WM) * (256 / WN);
-  constexpr int FM = WM / 32, FN = WN / 32;
-  constexpr int kBK = kDmaBK;
-  constexpr int kChunks = kBK / 2;             // 1 KB copies per operand and stage
-  constexpr int kPerWave = 2 * kChunks / kW;   // copies per wave and stage, both operands
-  static_assert((2 * kChunks) % kW == 0 && kChunks % kW == 0, "copies split evenly over the waves");
-
-  int s, tile;
-  int I, J;
-  split_tile<kMap>(blockIdx.x, S, ntiles, s, tile);
-  if constexpr (kMap == 2)
-    band_coords(tile, static_cast<int>(cdiv(static_cast<int64_t>(K), kTile)), I, J);
+template <bool kBF16>
+__device__ __forceinline__ void mfma32_asm(f32x16& acc, const u32x4& a, const u32x4& b) {
+  if constexpr (kBF16)
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
   else
-    tile_coords(tile, I, J);
+    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+// A wave-uniform 64-bit value through readfirstlane, which takes and returns
+// int: each half is widened as unsigned, so that a low half with bit 31 set
+// does not sign-extend into the high half.
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(v))));
+  const uint32_t hi =
+      static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(v >> 32))));
+  return static_cast<uint64_t>(hi) << 32 | lo;
+}
+
+// One 16-byte-per-lane copy into LDS from base + voff, zeros at and past nrec
+// bytes.  base and nrec are wave-uniform (the descriptor stays in SGPRs).
+// (Target builtins sit in a __device__ function, not in the kernel body: in
+// the kernel body the host pass dropped the kernel's launch stub.)
+__device__ __forceinline__ void lds_copy16(const uint16_t* base, uint32_t nrec, uint8_t* lds, uint32_t voff) {
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<uint16_t*>(uniform_u64(reinterpret_cast<uint64_t>(base))), static_cast<short>(0),
+      __builtin_amdgcn_readfirstlane(static_cast<int>(nrec)), 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)lds, 16, voff, 0, 0, 0);
+}
+
+__device__ __forceinline__ void bare_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// s_waitcnt for "at most N vector-memory operations outstanding" (gfx9
+// encoding: vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt left at "no wait")
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N < 64, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// s_waitcnt for "at most N LDS / scalar-memory operations outstanding"
+template <int N>
+__device__ __forceinline__ void wait_lgkm() {
+  static_assert(N < 16, "lgkmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0xC07F | (N << 8));
+}
+
+// copy slots: after which MFMA m of a step the step's j-th copy goes (-1:
+// none), and after which MFMA m (8..15) of the last step's tail
+constexpr int step_copy(int m) { return m % 4 == 1 ? m / 4 : -1; }
+constexpr int tail_copy(int m) { return m % 2 == 1 ? (m - 9) / 2 : -1; }
+
+template <bool kBF16>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void hessian_gram16(const uint16_t* __restrict__ X, int64_t n, int K, int64_t ldx, int S, int64_t tok_per_split,
+                    int ntiles, float* __restrict__ partial) {
+  constexpr int kBK = kDmaBK;
+  constexpr int kPerWave = kBK / 4;  // 12 copies of 1 KB per wave and stage: 6 of each operand
+
+  int s, tile, I, J;
+  split_tile<2>(blockIdx.x, S, ntiles, s, tile);
+  band_coords(tile, static_cast<int>(cdiv(static_cast<int64_t>(K), kTile)), I, J);
   const bool diag = (I == J);
-  const int nops = diag ? 1 : 2;
-  const int bop = diag ? 0 : 1;
-  const int64_t t_begin = static_cast<int64_t>(s) * tok_per_split;
-  const int64_t t_end = min(n, t_begin + tok_per_split);
+  const int64_t tb = static_cast<int64_t>(uniform_u64(static_cast<uint64_t>(static_cast<int64_t>(s) * tok_per_split)));
+  const int64_t te = static_cast<int64_t>(uniform_u64(static_cast<uint64_t>(min(n, tb + tok_per_split))));
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = (wave / (256 / WN)) * WM;
-  const int wn = (wave % (256 / WN)) * WN;
-  const bool wave_idle = diag && (wn >= wm + WM);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+  // the wave above the diagonal of a diagonal tile computes but stores nothing
+  const bool wave_idle = diag && wn > wm;
 
-  // copy role: chunk c of an operand holds token rows 2c, 2c + 1; lane l
-  // lands on row 2c + l / 32, slot l % 32, and fetches octet slot ^ sig(row)
+  // copy role: chunk c of an operand holds token rows 2c, 2c + 1; copy k
+  // (0..11) of this wave is chunk c = wave + 4 (k mod 6) of operand k / 6,
+  // all of one row parity.  Lane l lands on row 2c + l / 32, slot l % 32, and
+  // fetches octet slot ^ sig(row); features past K get an offset past every
+  // record count (zeros).
   const int64_t rowb = ldx * 2;
-  uint32_t vl[2][2];  // [operand][chunk parity]
+  uint32_t voff[kPerWave];
 #pragma unroll
-  for (int op = 0; op < 2; ++op)
+  for (int k = 0; k < kPerWave; ++k) {
+    const int op = k >= kPerWave / 2 ? 1 : 0;
+    const int c = wave + 4 * (k - op * (kPerWave / 2));
+    const int row = 2 * (wave & 1) + (lane >> 5);
+    const int oct = (lane & 31) ^ dma_sig(row);
+    const bool ok = (op == 0 ? I : J) * kTile + oct * 8 < K;
+    voff[k] = ok ? static_cast<uint32_t>((lane >> 5) * rowb + oct * 16 + 2 * c * rowb) : 0x80000000u;
+  }
+  // the two operands' bases and record counts for the stage at t0: rows past
+  // the split's end and the second operand of a diagonal tile are not fetched
+  struct StageSrc {
+    const uint16_t* base[2];
+    uint32_t nrec[2];
+  };
+  auto stage_src = [&](int64_t t0) {
+    const int rem = static_cast<int>(te - t0);
+    const int rows = rem <= 0 ? 0 : rem < kBK ? rem : kBK;
+    const uint32_t nrec = static_cast<uint32_t>(rows * rowb);
+    StageSrc ss;
 #pragma unroll
-    for (int par = 0; par < 2; ++par) {
-      const int row = 2 * par + (lane >> 5);
-      const int oct = (lane & 31) ^ dma_sig(row);
-      const bool ok = (op == 0 ? I : J) * kTile + oct * 8 < K;
-      vl[op][par] = ok ? static_cast<uint32_t>((lane >> 5) * rowb + oct * 16) : 0x80000000u;
+    for (int op = 0; op < 2; ++op) {
+      ss.base[op] = X + t0 * ldx + (op == 0 ? I : J) * kTile;
+      ss.nrec[op] = op == 1 && diag ? 0u : nrec;
     }
-  auto issue = [&](int64_t t0, auto bsel) {
-    constexpr int B = decltype(bsel)::value;
-    const int64_t left = t_end - t0;
-    const uint32_t nrec = static_cast<uint32_t>((left < kBK ? left : kBK) * rowb);
-#pragma unroll
-    for (int k = 0; k < kPerWave; ++k) {
-      const int id = wave + kW * k;  // chunk id over both operands
-      const int op = id / kChunks, c = id % kChunks;
-      if (op < nops) {
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint16_t*>(X + t0 * ldx + (op == 0 ? I : J) * kTile), static_cast<short>(0),
-            static_cast<int>(nrec), 0x00020000);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(hslab<B>(op) + c * 1024), 16,
-                                                 vl[op][c & 1] + static_cast<uint32_t>(2 * c * rowb), 0, 0, 0);
-      }
-    }
+    return ss;
+  };
+  auto copy = [&](const StageSrc& ss, auto bsel, auto ksel) {
+    constexpr int B = decltype(bsel)::value, k = decltype(ksel)::value;
+    constexpr int op = k >= kPerWave / 2 ? 1 : 0;
+    const int c = wave + 4 * (k - op * (kPerWave / 2));
+    lds_copy16(ss.base[op], ss.nrec[op], hslab<B>(op) + c * 1024, voff[k]);
   };
 
   // fragment role: lane (g, r, q) reads token 8 (g / 2) + r (+4 for the second
   // half), octet ob + 2 (g % 2) + q / 2, 8-byte half q % 2
   const int g = lane >> 4, r = (lane >> 2) & 3, q = lane & 3;
-  uint32_t aoff[FM], boff[FN];
+  const int bop = diag ? 0 : 1;
+  uint32_t aoff[4], boff[4];
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+  for (int i = 0; i < 4; ++i) {
     aoff[i] = (8 * (g >> 1) + r) * kRowB + ((((wm + 32 * i) >> 3) + 2 * (g & 1) + (q >> 1)) ^ dma_sig(r)) * 16 +
               (q & 1) * 8;
-#pragma unroll
-  for (int j = 0; j < FN; ++j)
-    boff[j] = (8 * (g >> 1) + r) * kRowB + ((((wn + 32 * j) >> 3) + 2 * (g & 1) + (q >> 1)) ^ dma_sig(r)) * 16 +
-              (q & 1) * 8;
+    boff[i] = bop * kStageB + (8 * (g >> 1) + r) * kRowB +
+              ((((wn + 32 * i) >> 3) + 2 * (g & 1) + (q >> 1)) ^ dma_sig(r)) * 16 + (q & 1) * 8;
+  }
 
-  f32x16 acc[FM][FN];
+  f32x16 acc[4][4];
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  auto compute = [&](const uint8_t* la, const uint8_t* lb) {
-    u32x4 fa[2][FM], fb[2][FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i) fa[0][i] = tr_frag(la + aoff[i]);
-#pragma unroll
-    for (int j = 0; j < FN; ++j) fb[0][j] = tr_frag(lb + boff[j]);
-#pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      const int cur = ks & 1;
-      if (ks + 1 < kBK / 16) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i) fa[cur ^ 1][i] = tr_frag(la + aoff[i] + (ks + 1) * 16 * kRowB);
-#pragma unroll
-        for (int j = 0; j < FN; ++j) fb[cur ^ 1][j] = tr_frag(lb + boff[j] + (ks + 1) * 16 * kRowB);
-      }
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          if constexpr (kBF16) {
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                __builtin_bit_cast(bf16x8, fa[cur][i]), __builtin_bit_cast(bf16x8, fb[cur][j]), acc[i][j], 0, 0, 0);
-          } else {
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                __builtin_bit_cast(f16x8, fa[cur][i]), __builtin_bit_cast(f16x8, fb[cur][j]), acc[i][j], 0, 0, 0);
-          }
-        }
-      __builtin_amdgcn_sched_barrier(0);
-    }
+  u32x4 fr[3][8];  // [set][A0..A3, B0..B3]
+  // fragment f of step ks of buffer B into set St; read order A0, B0, B1, B2,
+  // B3, A1, A2, A3 (the order the next step's MFMAs need them)
+  auto read = [&](auto bsel, auto ssel, auto ksel, auto fsel) {
+    constexpr int B = decltype(bsel)::value, St = decltype(ssel)::value;
+    constexpr int ks = decltype(ksel)::value, f = decltype(fsel)::value;
+    constexpr int idx = f == 0 ? 0 : f < 5 ? f + 3 : f - 4;
+    const uint8_t* base = hslab<B>(0) + ks * 16 * kRowB;
+    if constexpr (idx < 4)
+      fr[St][idx] = tr_frag(base + aoff[idx]);
+    else
+      fr[St][idx] = tr_frag(base + boff[idx - 4]);
   };
-  // one stage out of buffer B: wait until this wave's copies into B have
-  // landed (those of the next stage, in flight, may stay outstanding); after
-  // the barrier every wave's have, and no wave still reads buffer B + 2 (the
-  // previous stage's), which the copy of stage + 2 then fills
-  auto stage = [&](int64_t t0, auto bsel) {
-    constexpr int B = decltype(bsel)::value;
-    if (t0 + kBK >= t_end) wait_vm<0>();
-    else if (diag) wait_vm<kPerWave / 2>();
-    else wait_vm<kPerWave>();
-    __syncthreads();
-    if (t0 + 2 * kBK < t_end) issue(t0 + 2 * kBK, std::integral_constant<int, (B + 2) % 3>{});
-    if (!wave_idle) compute(hslab<B>(0), hslab<B>(bop));
+  auto mfma = [&](auto ssel, auto msel) {
+    constexpr int St = decltype(ssel)::value, m = decltype(msel)::value;
+    mfma32_asm<kBF16>(acc[m >> 2][m & 3], fr[St][m >> 2], fr[St][4 + (m & 3)]);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+
+  // one step on set St: 16 MFMAs; the next step's fragments (set Sn, step
+  // ksn of buffer Bn) after the first 8, copies 4j.. of the stage two ahead
+  // at the step's copy slots
+  auto step = [&](auto ssel, auto bnsel, auto snsel, auto knsel, const StageSrc& ss, auto psel, auto k0sel) {
+    sfor<0, 16>([&](auto mc) {
+      constexpr int m = decltype(mc)::value;
+      mfma(ssel, mc);
+      if constexpr (m < 8) read(bnsel, snsel, knsel, mc);
+      if constexpr (step_copy(m) >= 0)
+        copy(ss, psel, std::integral_constant<int, decltype(k0sel)::value + step_copy(m)>{});
+    });
+    sfor<0, 16>([&](auto mc) {
+      constexpr int m = decltype(mc)::value;
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                          // MFMA
+      if constexpr (m < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);      // LDS reads
+      if constexpr (step_copy(m) >= 0) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // copy
+    });
+    __builtin_amdgcn_sched_barrier(0);
   };
 
-  if (t_begin < t_end) {
-    issue(t_begin, std::integral_constant<int, 0>{});
-    if (t_begin + kBK < t_end) issue(t_begin + kBK, std::integral_constant<int, 1>{});
-    for (int64_t t0 = t_begin;;) {
-      stage(t0, std::integral_constant<int, 0>{});
-      if ((t0 += kBK) >= t_end) break;
-      stage(t0, std::integral_constant<int, 1>{});
-      if ((t0 += kBK) >= t_end) break;
-      stage(t0, std::integral_constant<int, 2>{});
-      if ((t0 += kBK) >= t_end) break;
+  // stage at t0 out of buffer B, its step-0 fragments already in set 0.  The
+  // tail after the barrier runs also after the split's last stage: its
+  // copies then have zero records and its reads go unused.
+  auto stage = [&](int64_t t0, auto bsel) {
+    constexpr int B = decltype(bsel)::value;
+    using Bn = std::integral_constant<int, (B + 1) % 3>;
+    using Bp = std::integral_constant<int, (B + 2) % 3>;
+    const StageSrc ahead2 = stage_src(t0 + 2 * kBK);
+    step(I0{}, bsel, I1{}, I1{}, ahead2, Bp{}, std::integral_constant<int, 4>{});
+    step(I1{}, bsel, I2{}, I2{}, ahead2, Bp{}, std::integral_constant<int, 8>{});
+    sfor<0, 8>([&](auto mc) { mfma(I2{}, mc); });
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm<kPerWave>();
+    wait_lgkm<0>();
+    bare_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    const StageSrc ahead3 = stage_src(t0 + 3 * kBK);
+    sfor<8, 16>([&](auto mc) {
+      constexpr int m = decltype(mc)::value;
+      mfma(I2{}, mc);
+      read(Bn{}, I0{}, I0{}, std::integral_constant<int, m - 8>{});
+      if constexpr (tail_copy(m) >= 0) copy(ahead3, bsel, std::integral_constant<int, tail_copy(m)>{});
+    });
+    sfor<8, 16>([&](auto mc) {
+      constexpr int m = decltype(mc)::value;
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      if constexpr (tail_copy(m) >= 0) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    });
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  if (tb < te) {
+    // stages 0 and 1 whole, copies 0..3 of stage 2 (the first stage's steps
+    // issue its copies 4..11)
+    const StageSrc s0 = stage_src(tb), s1 = stage_src(tb + kBK), s2 = stage_src(tb + 2 * kBK);
+    sfor<0, kPerWave>([&](auto kc) { copy(s0, I0{}, kc); });
+    sfor<0, kPerWave>([&](auto kc) { copy(s1, I1{}, kc); });
+    sfor<0, 4>([&](auto kc) { copy(s2, I2{}, kc); });
+    wait_vm<kPerWave + 4>();
+    bare_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    sfor<0, 8>([&](auto fc) { read(I0{}, I0{}, I0{}, fc); });
+    // three stages per trip, one per buffer; stages past the split's end
+    // multiply zeros, which leaves the sums unchanged (+0 added to a sum that
+    // starts at +0)
+    for (int64_t t0 = tb; t0 < te; t0 += 3 * kBK) {
+      stage(t0, I0{});
+      stage(t0 + kBK, I1{});
+      stage(t0 + 2 * kBK, I2{});
     }
+    // no copy may still be writing LDS when the workgroup ends
+    wait_vm<0>();
+    // the accumulators are read below: wait states after the last MFMA (the
+    // compiler does not see the asm MFMAs' results as MFMA results)
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   }
 
   // 32x32 accumulator layout: lane l, register v -> row 8*(v/4) + 4*(l/32) + v%4, col l%32
@@ -490,9 +602,9 @@ void hessian_dma16(const uint16_t* __restrict__ X, int64_t n, int K, int64_t ldx
   const int slot = I * (I + 1) / 2 + J;
   float* out = partial + (static_cast<int64_t>(s) * ntiles + slot) * (kTile * kTile);
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int row = wm + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
@@ -690,7 +802,9 @@ int accumulate_run(float* H, const void* X, int64_t n, int64_t K, int64_t ldx, i
   const int64_t per = cdiv(cdiv(n, S), 32) * 32;
   const dim3 grid(static_cast<unsigned>(S) * ntiles);
   const int esz = dtype_size(dtype);
-  const bool vec = (ldx * esz) % 16 == 0 && (reinterpret_cast<uintptr_t>(X) % 16) == 0 && (K * esz) % 16 == 0;
+  // (the DMA kernel's 32-bit row offsets: 48 rows of at most 8 MB)
+  const bool vec = (ldx * esz) % 16 == 0 && (reinterpret_cast<uintptr_t>(X) % 16) == 0 && (K * esz) % 16 == 0 &&
+                   ldx * esz <= (int64_t(1) << 23);
   if (dtype == GPTQ_F32) {
     const float* x = static_cast<const float*>(X);
     if (vec)
@@ -699,16 +813,16 @@ int accumulate_run(float* H, const void* X, int64_t n, int64_t K, int64_t ldx, i
       hipLaunchKernelGGL((hessian_tile32<false>), grid, dim3(kThreads), 0, st, x, n, (int)K, ldx, S, per, ntiles, part);
   } else {
     const uint16_t* x = static_cast<const uint16_t*>(X);
-    // aligned rows: LDS-DMA kernel, 8 waves of 128 x 64, split-major band order;
-    // otherwise the register-staged kernel with element loads
+    // aligned rows: LDS-DMA kernel, 4 waves of 128 x 128, split-major band
+    // order; otherwise the register-staged kernel with element loads
     if (dtype == GPTQ_BF16) {
       if (vec)
-        hipLaunchKernelGGL((hessian_dma16<true, 128, 64, 2>), grid, dim3(512), 0, st, x, n, (int)K, ldx, S, per, ntiles, part);
+        hipLaunchKernelGGL((hessian_gram16<true>), grid, dim3(256), 0, st, x, n, (int)K, ldx, S, per, ntiles, part);
       else
         hipLaunchKernelGGL((hessian_tile16<true, false>), grid, dim3(kThreads16), 0, st, x, n, (int)K, ldx, S, per, ntiles, part);
     } else {
       if (vec)
-        hipLaunchKernelGGL((hessian_dma16<false, 128, 64, 2>), grid, dim3(512), 0, st, x, n, (int)K, ldx, S, per, ntiles, part);
+        hipLaunchKernelGGL((hessian_gram16<false>), grid, dim3(256), 0, st, x, n, (int)K, ldx, S, per, ntiles, part);
       else
         hipLaunchKernelGGL((hessian_tile16<false, false>), grid, dim3(kThreads16), 0, st, x, n, (int)K, ldx, S, per, ntiles, part);
     }
