@@ -45,7 +45,7 @@ PEAK_HBM_GBS = 8000.0
 # counter passes over this script (FETCH_SIZE, then WRITE_SIZE), calibrated
 # against the hipMemcpy copies of known size in the same runs
 # (profiles/hessian_llama8b_block_traffic.md).
-HESSIAN_TRAFFIC = {"tokens": 262144, "read": 144.18e9, "written": 7.55e9}
+HESSIAN_TRAFFIC = {"tokens": 262144, "read": 105.70e9, "written": 7.55e9}
 
 HID, NQ, NKV, HD, FFN = 4096, 32, 8, 128, 14336
 
@@ -941,7 +941,7 @@ def main():
                        "hessian_tflops_in_block": round(tflops_blk, 1),
                        "hessian_kernel_ms_in_block": {k: round(v, 3) for k, v in b["hessian_kernel_ms"].items()},
                        "layer_losses": {k: round(v, 4) for k, v in b["losses"].items()}})
-        result["roofline"] = {"bound": "mfma", "kernel": "hessian_dma16 + hessian_reduce (down_proj input, alone)",
+        result["roofline"] = {"bound": "mfma", "kernel": "hessian_gram16 + hessian_reduce (down_proj input, alone)",
                               "achieved": round(tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                               "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
                               "launch_ms": round(b["hessian_iso_ms"], 3),

@@ -27,6 +27,12 @@ size_t hessian_split_bytes(int64_t K) {
 // (262144, 14336) -> 16, each within 5% of the best split count of a sweep
 // over 1..64, and 1.2-1.5x faster than ~2048 workgroups for the short calls;
 // bf16 at (262144, 4096): 16 / 24 / 32 splits 4.57 / 4.47 / 4.52 ms (26 now).
+// With the 4-wave tile kernel, (262144, 14336) with 4 / 8 / 12 / 16 splits
+// takes 41.6 / 41.8 / 42.6 / 42.9 ms.  A rule of up to 65536 tokens per split
+// was measured and not kept: its longer fp32 partial sums change H's rounding
+// (the 27685-token Hessian at K = 13824 ran as 1 split instead of 2, and the
+// 8-bit act-order codes then agreed with the fp32 oracle's to 0.99865, below
+// the 0.999 the validated rule meets), for 3% of the tile kernel's time.
 int choose_splits(int64_t n, int64_t ntiles) {
   constexpr int64_t kTokMin = 1024, kMinWG = 512;
   if (n <= 0 || ntiles <= 0) return 1;
