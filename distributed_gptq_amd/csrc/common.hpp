@@ -10,6 +10,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <string>
+#include <type_traits>
 
 #include "plan.hpp"
 
@@ -20,6 +21,16 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// f(std::integral_constant<int, i>) for i = I .. N - 1: an unrolled loop whose
+// index is a compile-time constant in the body (register arrays, LDS buffers)
+template <int I, int N, class F>
+__device__ __forceinline__ void sfor(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    sfor<I + 1, N>(f);
+  }
+}
 
 // -------------------------------------------------------------- errors ----
 // (set_error, clear_error and GPTQ_REQUIRE come from status.hpp)

@@ -356,14 +356,6 @@ __device__ __forceinline__ uint8_t* hslab(int op) {
   return B == 0 ? &g_hslab0[op][0] : B == 1 ? &g_hslab1[op][0] : &g_hslab2[op][0];
 }
 
-template <int I, int N, class F>
-__device__ __forceinline__ void sfor(F&& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>{});
-    sfor<I + 1, N>(f);
-  }
-}
-
 template <bool kBF16>
 __device__ __forceinline__ void mfma32_asm(f32x16& acc, const u32x4& a, const u32x4& b) {
   if constexpr (kBF16)

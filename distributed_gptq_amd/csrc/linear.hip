@@ -1063,6 +1063,56 @@ __device__ __forceinline__ uint4 dq_word_0415(uint32_t (&p)[4], uint32_t zz, uin
   return uint4{p[0], p[1], p[2], p[3]};
 }
 
+// The workgroup's scales and zeros (contiguous rows of the [N][ngroups]
+// arrays) staged once in LDS: per block a lane then reads its pairs from LDS
+// instead of 16-row gathers.  Element e = r ng + g of the rows' chunk goes to
+// sz[g][r].  Where both chunks are 16-byte aligned a lane loads 16 bytes of
+// each per round (8 halves or 4 floats; rows past N read as zeros through the
+// buffer descriptors) and steps (r, g) along them: one round for up to 4096
+// halves per array, where one element pair per lane and round made the
+// staging a chain of memory round trips.  kPer threads take part.
+template <int NT>
+__device__ __forceinline__ void stage_sz(const LinArgs& a, int64_t n0, float2* sz, int tid, int lane, int kPer) {
+  const int ng = static_cast<int>(a.ngroups);
+  const int tot = NT * ng;
+  const int esz = a.sz_dtype == GPTQ_F32 ? 4 : 2;
+  const char* sb = static_cast<const char*>(a.scales) + n0 * a.ngroups * esz;
+  const char* zb = static_cast<const char*>(a.zeros) + n0 * a.ngroups * esz;
+  if (((reinterpret_cast<uintptr_t>(sb) | reinterpret_cast<uintptr_t>(zb)) & 15u) == 0) {
+    const uint32_t bytes = static_cast<uint32_t>(std::min<int64_t>(NT, a.N - n0) * ng * esz);
+    const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb, bytes), zrs = make_rsrc(zb, bytes);
+    const int epv = 16 / esz;
+    const int nvec = static_cast<int>(cdiv(tot, epv));
+    for (int v = tid; v - lane < nvec; v += kPer) {
+      const uint32_t off = 16u * static_cast<uint32_t>(v);
+      const u32x4 sv = __builtin_amdgcn_raw_buffer_load_b128(srs, off, 0, 0);
+      const u32x4 zv = __builtin_amdgcn_raw_buffer_load_b128(zrs, off, 0, 0);
+      const int e0 = v * epv;
+      if (e0 >= tot) continue;
+      int r = e0 / ng, g = e0 - r * ng;
+      auto put = [&](float sv_, float zv_) {
+        if (r < NT) sz[g * NT + r] = float2{sv_, zv_};
+        if (++g == ng) { g = 0; ++r; }
+      };
+      if (esz == 4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) put(__builtin_bit_cast(float, sv[j]), __builtin_bit_cast(float, zv[j]));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          put(elem_value((sv[j / 2] >> (16 * (j & 1))) & 0xFFFFu, false, a.sz_dtype),
+              elem_value((zv[j / 2] >> (16 * (j & 1))) & 0xFFFFu, false, a.sz_dtype));
+      }
+    }
+  } else {
+    for (int e = tid; e < tot; e += kPer) {
+      const int64_t off = std::min<int64_t>(n0 + e / ng, a.N - 1) * a.ngroups + e % ng;
+      sz[(e % ng) * NT + e / ng] =
+          float2{load_elem(a.scales, off, a.sz_dtype), load_elem(a.zeros, off, a.sz_dtype)};
+    }
+  }
+}
+
 // kFold (group size a multiple of 128, so a block is one group): the codes
 // enter the MFMA as small integers (fp16: q, from 1024 + q less 1024; bf16:
 // 128 + q straight from the OR, exact in bf16), products are exact in fp32,
@@ -1086,8 +1136,6 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
   const int kb0 = static_cast<int>(blockIdx.y) * bps;
   const int nblk = std::min(ktot - kb0, bps);
   const int r16 = lane & 15, g4 = lane >> 4;
-  const int ng = static_cast<int>(a.ngroups);
-
 
   const uint8_t* wrow[BN];
   int64_t wn[BN];
@@ -1199,54 +1247,7 @@ __global__ __launch_bounds__(64 * WAVES) void dq_reg4_k(LinArgs a) {
   if (b < nblk) load(b, A);
   if (b + WAVES < nblk) load(b + WAVES, B);
 
-  // the workgroup's scales and zeros (contiguous rows of the [N][ngroups]
-  // arrays) are staged once in LDS: per block a lane then reads its pairs
-  // from LDS instead of 16-row gathers.  Element e = r ng + g of the rows'
-  // chunk goes to sz[g][r].  Where both chunks are 16-byte aligned a lane
-  // loads 16 bytes of each per round (8 halves or 4 floats; rows past N read
-  // as zeros through the buffer descriptors) and steps (r, g) along them:
-  // one round for up to 4096 halves per array, where one element pair per
-  // lane and round made the staging a chain of memory round trips
-  {
-    constexpr int kPer = 64 * WAVES;
-    const int tot = NT * ng;
-    const int esz = a.sz_dtype == GPTQ_F32 ? 4 : 2;
-    const char* sb = static_cast<const char*>(a.scales) + n0 * a.ngroups * esz;
-    const char* zb = static_cast<const char*>(a.zeros) + n0 * a.ngroups * esz;
-    if (((reinterpret_cast<uintptr_t>(sb) | reinterpret_cast<uintptr_t>(zb)) & 15u) == 0) {
-      const uint32_t bytes = static_cast<uint32_t>(std::min<int64_t>(NT, a.N - n0) * ng * esz);
-      const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb, bytes), zrs = make_rsrc(zb, bytes);
-      const int epv = 16 / esz;
-      const int nvec = static_cast<int>(cdiv(tot, epv));
-      for (int v = tid; v - lane < nvec; v += kPer) {
-        const uint32_t off = 16u * static_cast<uint32_t>(v);
-        const u32x4 sv = __builtin_amdgcn_raw_buffer_load_b128(srs, off, 0, 0);
-        const u32x4 zv = __builtin_amdgcn_raw_buffer_load_b128(zrs, off, 0, 0);
-        const int e0 = v * epv;
-        if (e0 >= tot) continue;
-        int r = e0 / ng, g = e0 - r * ng;
-        auto put = [&](float sv_, float zv_) {
-          if (r < NT) sz[g * NT + r] = float2{sv_, zv_};
-          if (++g == ng) { g = 0; ++r; }
-        };
-        if (esz == 4) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) put(__builtin_bit_cast(float, sv[j]), __builtin_bit_cast(float, zv[j]));
-        } else {
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-            put(elem_value((sv[j / 2] >> (16 * (j & 1))) & 0xFFFFu, false, a.sz_dtype),
-                elem_value((zv[j / 2] >> (16 * (j & 1))) & 0xFFFFu, false, a.sz_dtype));
-        }
-      }
-    } else {
-      for (int e = tid; e < tot; e += kPer) {
-        const int64_t off = std::min<int64_t>(n0 + e / ng, a.N - 1) * a.ngroups + e % ng;
-        sz[(e % ng) * NT + e / ng] =
-            float2{load_elem(a.scales, off, a.sz_dtype), load_elem(a.zeros, off, a.sz_dtype)};
-      }
-    }
-  }
+  stage_sz<NT>(a, n0, sz, tid, lane, 64 * WAVES);
   __syncthreads();
 
   for (bool first = true;; first = false) {
@@ -1324,6 +1325,195 @@ int launch_reg4(hipStream_t st, const LinArgs& a, int splits = 1) {
   hipLaunchKernelGGL(splitk_reduce_k, dim3(static_cast<unsigned>(cdiv(quads, 256))), dim3(256), 0, st, a.part, splits,
                      a.M, a.N, a.bias, a.bias_dtype, static_cast<void*>(a.y), a.y_dtype);
   return check_launch("splitk_reduce");
+}
+
+// M <= 16 on wide layers (N >= 14336, K <= 4096, groups of >= 128 columns,
+// 4- or 3-bit codes): each wave owns 16 weight rows over the whole of K and
+// streams its rows' codes through a ring of D register slots (loads clamped
+// to the last block, so every slot is refilled unconditionally and each wait
+// covers one slot's load), decoding them as dq_reg4_k's kFold path does.  X
+// (16 x K, rows past M as zeros) is staged once per workgroup in LDS, already
+// in the lanes' order (perm_0415 per 16 bytes: slot [b][g][kk][r] holds X row
+// r, columns 128 b + 32 g + 8 kk .. + 7), with the per-block sums of X from
+// the same all-ones MFMA chain.  No K split and no cross-wave reduction: a
+// wave's 16 x 16 tile is summed over the blocks in order and stored.  In
+// dq_reg4_k the waves of a workgroup split K, so each streamed 4 of the 32
+// blocks at 28672 x 4096 with two in flight, and the prologue and the
+// cross-wave reduction took about half of the launch.
+constexpr int kRow16MaxBlk = 32;  // K <= 4096: X takes 128 KB of LDS
+__shared__ __attribute__((aligned(16))) uint4 g_row16_x[kRow16MaxBlk * 256];
+__shared__ float g_row16_sx[kRow16MaxBlk][16];
+
+template <int BITS, int W, int D, bool BF16>
+__global__ __launch_bounds__(64 * W) void dq_row16_k(LinArgs a) {
+  constexpr int NT = 16 * W;
+  extern __shared__ __attribute__((aligned(16))) float2 sz[];  // [ngroups][NT]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * NT;
+  const int nblk = static_cast<int>(a.K / 128);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const uint8_t* wrow = a.packed + std::min<int64_t>(n0 + 16 * wave + r16, a.N - 1) * a.pitch;
+
+  auto mfma = [](uint4 fa, uint4 fb, f32x4 c) {
+    if constexpr (BF16)
+      return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, fa), __builtin_bit_cast(bf16x8, fb), c,
+                                                     0, 0, 0);
+    else
+      return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, fa), __builtin_bit_cast(f16x8, fb), c, 0,
+                                                    0, 0);
+  };
+
+  // X into LDS in the lanes' order.  All of a thread's loads are issued
+  // before any is waited for (in batches of kXB), and before the code
+  // prefetch, so that waiting for them leaves the code loads in flight.
+  // Slots past the last block repeat the last one and rows past M are
+  // zeroed after the load: every load and store is unconditional, which
+  // keeps the compiler's waits exact.
+  {
+    constexpr int kXB = 64 * W >= 448 ? 20 : 16;  // 8192 slots / threads, per batch
+    const int tot = nblk * 256;
+    for (int base = tid; base < tot; base += kXB * 64 * W) {
+      uint4 v[kXB];
+#pragma unroll
+      for (int j = 0; j < kXB; ++j) {
+        const int idx = std::min(base + j * 64 * W, tot - 1);
+        const int b = idx >> 8, g = (idx >> 6) & 3, kk = (idx >> 4) & 3, r = idx & 15;
+        const int row = r < a.M ? r : 0;
+        v[j] = *reinterpret_cast<const uint4*>(a.x + static_cast<int64_t>(row) * a.K + b * 128 + 32 * g + 8 * kk);
+      }
+#pragma unroll
+      for (int j = 0; j < kXB; ++j) {
+        const int idx = std::min(base + j * 64 * W, tot - 1);
+        const uint4 pv = perm_0415(v[j]);
+        const bool live = (idx & 15) < a.M;
+        g_row16_x[idx] = uint4{live ? pv.x : 0u, live ? pv.y : 0u, live ? pv.z : 0u, live ? pv.w : 0u};
+      }
+    }
+  }
+
+  // slot loads: codes 32 g4 .. 32 g4 + 31 of block b (clamped) of the lane's row
+  uint32_t cw[D][BITS];
+  auto load = [&](int b, auto slot) {
+    constexpr int S = decltype(slot)::value;
+    b = std::min(b, nblk - 1);
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(wrow + static_cast<int64_t>(b * 128 + 32 * g4) * BITS / 8);
+    if constexpr (BITS == 4) {
+      const uint4 v = *reinterpret_cast<const uint4*>(src);
+      cw[S][0] = v.x; cw[S][1] = v.y; cw[S][2] = v.z; cw[S][3] = v.w;
+    } else {
+      cw[S][0] = src[0]; cw[S][1] = src[1]; cw[S][2] = src[2];
+    }
+  };
+  sfor<0, D>([&](auto sc) { load(decltype(sc)::value, sc); });
+
+  stage_sz<NT>(a, n0, sz, tid, lane, 64 * W);
+  __syncthreads();
+  // the blocks' sums of X (X row l % 16 in every register of lane l)
+  for (int b = wave; b < nblk; b += W) {
+    constexpr uint32_t kOne = BF16 ? 0x3f803f80u : 0x3c003c00u;
+    f32x4 t = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) t = mfma(uint4{kOne, kOne, kOne, kOne}, g_row16_x[((b * 4 + g4) * 4 + kk) * 16 + r16], t);
+    if (g4 == 0) g_row16_sx[b][r16] = t[0];
+  }
+  __syncthreads();
+
+  // a block's LDS operands (X fragments, sum of X, scales and zeros of the
+  // lane's four rows), read one block ahead of their MFMAs
+  struct Lds {
+    uint4 x[4];
+    float sx;
+    float4 p01, p23;
+  };
+  auto fetch = [&](int b, Lds& L) {
+    b = std::min(b, nblk - 1);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) L.x[kk] = g_row16_x[((b * 4 + g4) * 4 + kk) * 16 + r16];
+    L.sx = g_row16_sx[b][r16];
+    const float2* szg = sz + __builtin_amdgcn_readfirstlane(b * 128 / a.gs) * NT + 16 * wave;
+    L.p01 = *reinterpret_cast<const float4*>(szg + 4 * g4);
+    L.p23 = *reinterpret_cast<const float4*>(szg + 4 * g4 + 2);
+  };
+
+  // codes enter as 128 + q (bf16) or 1024 + q (fp16) from an AND-OR; the
+  // offset joins the zero in the per-row correction s (sum q' x - z' sum x)
+  uint32_t mask = BITS == 3 ? 0x00070007u : 0x000F000Fu, magic = BF16 ? 0x43004300u : 0x64006400u;
+  asm volatile("" : "+v"(mask), "+v"(magic));
+  constexpr float kZoff = BF16 ? 128.0f : 1024.0f;
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto block = [&](const Lds& L, auto slot) {
+    constexpr int S = decltype(slot)::value;
+    f32x4 t = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      uint32_t q[4];
+      step_fields<BITS>(cw[S], kk, q);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) q[u] = (q[u] & mask) | magic;
+      t = mfma(uint4{q[0], q[1], q[2], q[3]}, L.x[kk], t);
+    }
+    const float ps[4] = {L.p01.x, L.p01.z, L.p23.x, L.p23.z}, pz[4] = {L.p01.y, L.p01.w, L.p23.y, L.p23.w};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[v] = fmaf(ps[v], fmaf(-(pz[v] + kZoff), L.sx, t[v]), acc[v]);
+  };
+  // slots of an even ring alternate the two LDS operand sets.  Trips of D
+  // blocks refill each slot after use while D more blocks remain; the last
+  // (up to D) blocks drain the ring with no loads, so that every trip's
+  // loads are unconditional and each wait covers exactly one slot
+  static_assert(D % 2 == 0, "ring of an even number of slots");
+  Lds L0, L1;
+  fetch(0, L0);
+  auto trip = [&](int b0, auto refill) {
+    sfor<0, D>([&](auto sc) {
+      constexpr int S = decltype(sc)::value;
+      Lds& cur = S % 2 == 0 ? L0 : L1;
+      Lds& nxt = S % 2 == 0 ? L1 : L0;
+      fetch(b0 + S + 1, nxt);
+      // the next block's LDS reads go out before this block's decode and
+      // MFMAs (left alone, the compiler sank them below the MFMAs and waited
+      // for them at the top of the next block)
+      __builtin_amdgcn_sched_barrier(0);
+      if (b0 + S < nblk) block(cur, sc);
+      if constexpr (decltype(refill)::value) load(b0 + S + D, sc);
+    });
+  };
+  int b0 = 0;
+  for (; b0 + D < nblk; b0 += D) trip(b0, std::true_type{});
+  trip(b0, std::false_type{});
+
+  // 16x16 layout: lane l, register v -> W row 4 (l / 16) + v, X row l % 16
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int64_t m = r16, n = n0 + 16 * wave + 4 * g4 + v;
+    if (m < a.M && n < a.N) {
+      float r = acc[v];
+      if (a.bias) r += load_elem(a.bias, n, a.bias_dtype);
+      store_elem(a.y, m * a.N + n, a.y_dtype, r);
+    }
+  }
+}
+
+// a ring of 4 slots: at 28672 x 4096, M = 16 / 2 (4-bit), 2 / 4 / 6 / 8 / 16 /
+// 32 slots took 22.3 / 19.7 / 20.3 / 20.6 / 22.5 / 26.5 and 20.3 / 17.8 /
+// 18.5 / 18.9 / 20.9 / 24.6 us (refilling pairs of slots together, so that
+// both halves of each 128-byte line go out back to back, changed nothing)
+template <int BITS, int W, bool BF16>
+int launch_row16(hipStream_t st, const LinArgs& a) {
+  constexpr int D = 4;
+  const size_t lds = static_cast<size_t>(16 * W) * a.ngroups * sizeof(float2);
+  const dim3 grid(static_cast<unsigned>(cdiv(a.N, 16 * W)));
+  hipLaunchKernelGGL((dq_row16_k<BITS, W, D, BF16>), grid, dim3(64 * W), lds, st, a);
+  return check_launch("dq_row16");
+}
+
+// dq_row16_k takes the layer when X and the workgroup's scales and zeros fit
+// the LDS beside each other and the layer is wide enough to fill the CUs
+inline bool row16_fits(const LinArgs& a, int W) {
+  const size_t stat = sizeof(uint4) * kRow16MaxBlk * 256 + sizeof(float) * kRow16MaxBlk * 16;
+  return a.K % 128 == 0 && a.K <= 128 * kRow16MaxBlk && a.gs % 128 == 0 &&
+         stat + static_cast<size_t>(16 * W) * a.ngroups * sizeof(float2) <= 160 * 1024;
 }
 
 // (K splits of the register path on 4097-8192-row layers, 1 < M <= 16:
@@ -1881,8 +2071,17 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
         // two (measured at 28672 x 4096, M = 16 / 8 / 2: 26.4 / 24.1 / 22.5 us
         // against 26.8 / 25.1 / 23.6 (4-bit), 26.9 / 25.6 / 24.2 against
         // 28.8 / 27.1 / 26.1 (3-bit))
+        // Where K <= 4096 and groups span >= 128 columns, dq_row16_k's 7 waves
+        // of 16 rows over all of K: 28672 x 4096 at M = 16 / 2 19.7 / 17.8
+        // against 23.6 / 20.1 us (4-bit), 22.8 / 20.7 against 24.6 / 22.6
+        // (3-bit); slower at 14336 rows (16.9 against 14.9 us at M = 16 with
+        // 4 waves, 1 per SIMD) and with 8 waves of 224 workgroups at 28672
+        // rows (23.5 us)
         const int64_t w112 = cdiv(a.N, 112);
-        if (w112 > 240 && w112 <= 256 && a.ngroups <= 64) return launch_reg4<BITS, 112, 8, BF16>(st, a);
+        if (w112 > 240 && w112 <= 256 && a.ngroups <= 64) {
+          if (row16_fits(a, 7)) return launch_row16<BITS, 7, BF16>(st, a);
+          return launch_reg4<BITS, 112, 8, BF16>(st, a);
+        }
         return launch_reg4<BITS, 64, 4, BF16>(st, a);
       }
       if (a.N >= 32 * 256) {
