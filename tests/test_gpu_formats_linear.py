@@ -498,6 +498,30 @@ def test_linear_small_m_wide_n(hip, xdt, bits, gs, M, N):
     check_linear(y, x, codes, scales, zeros, np.arange(K) // gs, bias, bits=bits)
 
 
+@pytest.mark.parametrize("M,N,K,gs,bits,xdt", [
+    (16, 28672 - 37, 4096, 128, 4, torch.float16),
+    (5, 28672 - 37, 4096, 256, 3, torch.bfloat16),
+    (2, 26881, 1024, 128, 4, torch.bfloat16),
+    (16, 26881, 2048, 128, 3, torch.float16),
+    (11, 28672, 1024, 256, 4, torch.float16),
+    (16, 28672, 4096, 128, 3, torch.bfloat16),
+    (1, 28672 - 37, 4096, 128, 4, torch.bfloat16),
+])
+def test_linear_row16(hip, M, N, K, gs, bits, xdt):
+    """The 241-256-workgroup class of M <= 16 (dq_row16_k: 7 waves of 16 rows
+    over all of K, X staged once per workgroup): ragged N (a last workgroup
+    of 75 rows, and of 1 row at N = 26881), K of 1024-4096 (8-32 blocks
+    through a ring of 4 slots), groups of 128 and 256 columns, M below 16
+    (rows of X past M zero in LDS), bias, 3/4-bit, fp16/bf16.  The M = 1
+    case takes the M = 1 GEMV at the same shape, the others dq_row16_k."""
+    from distributed_gptq_amd import _ops
+    codes, scales, zeros, x = _case(M, N, K, bits, gs, M + N + K + bits, xdt)
+    bias = torch.randn(N).to(xdt)
+    packed = torch.from_numpy(O.pack_bitstream(codes, bits)).cuda()
+    y = _ops.linear(x.cuda(), packed, bits, scales.cuda(), zeros.cuda(), K, group_size=gs, bias=bias.cuda())
+    check_linear(y, x, codes, scales, zeros, np.arange(K) // gs, bias, bits=bits)
+
+
 _C4 = {}
 
 
