@@ -2,9 +2,9 @@
 //
 // Work decomposition
 //   * H is cut into 256 x 256 tiles; only tiles (I, J) with J <= I are
-//     computed.  A tile is one workgroup of 8 waves in a 2 x 4 grid, each
-//     wave owning a 128 x 64 block = 4 x 2 MFMA 32x32 blocks (128 fp32
-//     accumulators per lane).
+//     computed.  A tile is one workgroup of 4 waves (one per SIMD) in a 2 x 2
+//     grid, each wave owning a 128 x 128 block = 4 x 4 MFMA 32x32 blocks (256
+//     fp32 accumulators per lane, in AGPRs).
 //   * The tokens are cut into S contiguous splits (choose_splits: at most
 //     16384 tokens each).  Workgroup b works on the (split, tile) pair that
 //     split_tile maps it to: split-major, tiles in band order, each round of
@@ -15,11 +15,14 @@
 //
 // Operands.  The Gram matrix needs, per lane, 8 consecutive tokens of one
 // feature (the k-run of v_mfma_f32_32x32x16_{bf16,f16}); X is stored token-
-// major, so every thread loads an 8 token x 8 feature block with eight
-// 128-bit loads, transposes it in registers and writes eight 128-bit feature
-// runs to LDS.  The LDS slot of feature f is f ^ ((f >> 4) & 15), which keeps
-// both the transposed writes and the MFMA-fragment reads free of 16-byte
-// bank-group collisions.  fp32 inputs use v_mfma_f32_32x32x2_f32 with a
+// major.  With 16-byte aligned rows (hessian_gram16) token rows are copied
+// into LDS as they are (direct-to-LDS buffer loads) and the fragments are
+// read back transposed with ds_read_b64_tr_b16.  Otherwise (hessian_tile16)
+// every thread loads an 8 token x 8 feature block with eight loads,
+// transposes it in registers and writes eight 128-bit feature runs to LDS;
+// there the LDS slot of feature f is swz(f) (below), which keeps both the
+// transposed writes and the MFMA-fragment reads free of 16-byte bank-group
+// collisions.  fp32 inputs use v_mfma_f32_32x32x2_f32 with a
 // token-major LDS tile (no transpose needed).
 #include <type_traits>
 
