@@ -1327,8 +1327,9 @@ int launch_reg4(hipStream_t st, const LinArgs& a, int splits = 1) {
   return check_launch("splitk_reduce");
 }
 
-// M <= 16 on wide layers (N >= 14336, K <= 4096, groups of >= 128 columns,
-// 4- or 3-bit codes): each wave owns 16 weight rows over the whole of K and
+// M <= 16 on layers of 241-256 workgroups of 112 rows (26881-28672 rows; K <=
+// 4096, groups of >= 128 columns, 4- or 3-bit codes): each wave owns 16
+// weight rows over the whole of K and
 // streams its rows' codes through a ring of D register slots (loads clamped
 // to the last block, so every slot is refilled unconditionally and each wait
 // covers one slot's load), decoding them as dq_reg4_k's kFold path does.  X
@@ -1508,8 +1509,8 @@ int launch_row16(hipStream_t st, const LinArgs& a) {
   return check_launch("dq_row16");
 }
 
-// dq_row16_k takes the layer when X and the workgroup's scales and zeros fit
-// the LDS beside each other and the layer is wide enough to fill the CUs
+// dq_row16_k's layout: K a multiple of 128 up to 4096, one group per block,
+// and X, the block sums and the workgroup's scales and zeros within the LDS
 inline bool row16_fits(const LinArgs& a, int W) {
   const size_t stat = sizeof(uint4) * kRow16MaxBlk * 256 + sizeof(float) * kRow16MaxBlk * 16;
   return a.K % 128 == 0 && a.K <= 128 * kRow16MaxBlk && a.gs % 128 == 0 &&
