@@ -1329,10 +1329,10 @@ int launch_reg4(hipStream_t st, const LinArgs& a, int splits = 1) {
 
 // M <= 16 on layers of 241-256 workgroups of 112 rows (26881-28672 rows; K <=
 // 4096, groups of >= 128 columns, 4- or 3-bit codes): each wave owns 16
-// weight rows over the whole of K and
-// streams its rows' codes through a ring of D register slots (loads clamped
-// to the last block, so every slot is refilled unconditionally and each wait
-// covers one slot's load), decoding them as dq_reg4_k's kFold path does.  X
+// weight rows over the whole of K and streams its rows' codes through a ring
+// of D register slots (loads clamped to the last block, so every slot is
+// refilled unconditionally and each wait covers one slot's load), decoding
+// them as dq_reg4_k's kFold path does.  X
 // (16 x K, rows past M as zeros) is staged once per workgroup in LDS, already
 // in the lanes' order (perm_0415 per 16 bytes: slot [b][g][kk][r] holds X row
 // r, columns 128 b + 32 g + 8 kk .. + 7), with the per-block sums of X from
