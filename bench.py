@@ -45,7 +45,7 @@ PEAK_HBM_GBS = 8000.0
 # counter passes over this script (FETCH_SIZE, then WRITE_SIZE), calibrated
 # against the hipMemcpy copies of known size in the same runs
 # (profiles/hessian_llama8b_block_traffic.md).
-HESSIAN_TRAFFIC = {"tokens": 262144, "read": 105.70e9, "written": 7.55e9}
+HESSIAN_TRAFFIC = {"tokens": 262144, "read": 91.61e9, "written": 2.50e9}
 
 HID, NQ, NKV, HD, FFN = 4096, 32, 8, 128, 14336
 

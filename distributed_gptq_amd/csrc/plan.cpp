@@ -28,17 +28,23 @@ size_t hessian_split_bytes(int64_t K) {
 // over 1..64, and 1.2-1.5x faster than ~2048 workgroups for the short calls;
 // bf16 at (262144, 4096): 16 / 24 / 32 splits 4.57 / 4.47 / 4.52 ms (26 now).
 // With the 4-wave tile kernel, (262144, 14336) with 4 / 8 / 12 / 16 splits
-// takes 41.6 / 41.8 / 42.6 / 42.9 ms.  A rule of up to 65536 tokens per split
-// was measured and not kept: its longer fp32 partial sums change H's rounding
-// (the 27685-token Hessian at K = 13824 ran as 1 split instead of 2, and the
-// 8-bit act-order codes then agreed with the fp32 oracle's to 0.99865, below
-// the 0.999 the validated rule meets), for 3% of the tile kernel's time.
+// takes 41.6 / 41.8 / 42.6 / 42.9 ms, and the reduce reads 4x fewer partial
+// tiles with 4: products of >= 1024 tiles (K >= 11265) therefore take at most
+// 4 splits, or as many as keep each <= 65536 tokens (tile + reduce at
+// (262144, 14336): 43.1 against 44.7 ms; workspace 1.7 against 6.7 GB).
+// Shorter products keep the rule above: applied to every product, 65536
+// tokens per split changed H's rounding where the sweeps were validated (the
+// 27685-token Hessian at K = 13824 ran as 1 split instead of 2, and the 8-bit
+// act-order codes then agreed with the fp32 oracle's to 0.99865, below 0.999).
 int choose_splits(int64_t n, int64_t ntiles) {
   constexpr int64_t kTokMin = 1024, kMinWG = 512;
   if (n <= 0 || ntiles <= 0) return 1;
   const int64_t tok_max = ntiles < 512 ? 10240 : 16384;
   const int64_t fill = std::min<int64_t>(ceil_div(kMinWG, ntiles), std::max<int64_t>(1, n / kTokMin));
-  const int64_t s = std::max<int64_t>(ceil_div(n, tok_max), fill);
+  int64_t s = std::max<int64_t>(ceil_div(n, tok_max), fill);
+  // >= 1024 tiles: 4 splits already make >= 4096 workgroups (16 rounds of the
+  // 256 CUs), so beyond 4 only as many as keep each split <= 65536 tokens
+  if (ntiles >= 1024) s = std::max<int64_t>(std::min<int64_t>(s, 4), ceil_div(n, 65536));
   return static_cast<int>(std::min<int64_t>(std::max<int64_t>(s, 1), 64));
 }
 

@@ -48,8 +48,14 @@ static void hessian_checks() {
     for (int64_t n : kSizes) {
       const int S = plan::choose_splits(n, nt);
       CHECK(S >= 1 && S <= 64, "choose_splits(%" PRId64 ", %" PRId64 ") = %d", n, nt, S);
-      const int64_t tok_max = nt < 512 ? 10240 : 16384;
+      // tokens per split: <= 10240 below 512 tiles, <= 16384 below 1024, and
+      // from 1024 tiles on <= 65536 with at least 4 splits of > 16384
+      const int64_t tok_max = nt < 512 ? 10240 : nt < 1024 ? 16384 : 65536;
       CHECK(S == 64 || S >= plan::ceil_div(n, tok_max), "too few splits for n=%" PRId64, n);
+      if (nt >= 1024) {
+        CHECK(S == 64 || S >= std::min<int64_t>(4, plan::ceil_div(n, 16384)), "too few splits for n=%" PRId64, n);
+        CHECK(S <= std::max<int64_t>(4, plan::ceil_div(n, 65536)), "too many splits for n=%" PRId64, n);
+      }
       const size_t ws = gptq_hessian_workspace_size(n, K);
       std::printf("gptq_hessian_workspace_size %" PRId64 " %" PRId64 " = %zu\n", n, K, ws);
       CHECK(ws == static_cast<size_t>(S) * mn, "workspace_size(%" PRId64 ", %" PRId64 ")", n, K);

@@ -47,6 +47,36 @@ def test_hessian_many_splits(hip, dtype):
     assert torch.equal(H, H.T)
 
 
+@pytest.mark.parametrize("n,S", [(70000 + 13, 4), (262144 + 37, 5)])
+def test_hessian_long_splits(hip, n, S):
+    """A product of >= 1024 tiles (K = 11520: 45 x 46 / 2 = 1035 tiles of 256)
+    takes at most 4 token splits, or as many as keep each <= 65536 tokens:
+    17504 and 52437 tokens of fp32 accumulation per split here.  H within 1e-5
+    of the fp64 Gram matrix (computed on the GPU in fp64) and exactly
+    symmetric."""
+    from distributed_gptq_amd import _lib, _ops
+    K = 11520
+    lib = _lib.lib()
+    assert lib.gptq_hessian_workspace_size(n, K) == S * lib.gptq_hessian_workspace_min(K)
+    g = torch.Generator(device="cuda").manual_seed(n)
+    X = torch.randn(n, K, generator=g, device="cuda")
+    X[:, 11] *= 30
+    X[:, 4000:4008] *= 5
+    Xd = X.to(torch.bfloat16)
+    del X
+    H = torch.zeros(K, K, device="cuda")
+    _ops.hessian_accumulate(H, Xd)
+    X64 = Xd.double()
+    H64 = X64.t() @ X64
+    del X64
+    rel = float(torch.linalg.norm(H.double() - H64) / torch.linalg.norm(H64))
+    print(f"n={n} K={K} splits={S}: |H - H64| / |H64| = {rel:.2e}")
+    assert rel < 1e-5, rel
+    assert torch.equal(H, H.t())
+    del H64, Xd
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("cap_splits", [1, 3])
 def test_hessian_bounded_workspace(hip, dtype, cap_splits):
