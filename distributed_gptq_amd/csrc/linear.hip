@@ -1843,19 +1843,28 @@ __global__ __launch_bounds__(64 * (WAVES + L)) __attribute__((amdgpu_waves_per_e
     if (pk) {
       const int64_t g_lo = static_cast<int64_t>(kb0) * 128 / a.gs;
       const int64_t g_hi = std::min<int64_t>(a.ngroups, (static_cast<int64_t>(kb0 + nblk) * 128 - 1) / a.gs + 1);
+      // fp16 zeros (pk requires them); the check combines with `&`, not
+      // `&&`: a short-circuit let the compiler load each zero only after the
+      // previous one passed, a chain of 8 NB dependent loads with 32 rows per
+      // wave (the same time at the config-4 shapes, where they hit the cache;
+      // now one round trip whatever the cache holds)
+      const _Float16* zh = static_cast<const _Float16*>(a.zeros);
+      bool ok = true;
       for (int64_t g0 = g_lo + g4; g0 < g_hi; g0 += 32) {
         float z[8][NB];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           const int64_t g = std::min<int64_t>(g0 + 4 * u, g_hi - 1);
 #pragma unroll
-          for (int i = 0; i < NB; ++i) z[u][i] = load_elem(a.zeros, wn[i] * a.ngroups + g, a.sz_dtype);
+          for (int i = 0; i < NB; ++i) z[u][i] = static_cast<float>(zh[wn[i] * a.ngroups + g]);
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u)
 #pragma unroll
-          for (int i = 0; i < NB; ++i) pk = pk && z[u][i] == rintf(z[u][i]) && z[u][i] >= 0.0f && z[u][i] <= 1023.0f;
+          for (int i = 0; i < NB; ++i)
+            ok = ok & (z[u][i] == rintf(z[u][i])) & (z[u][i] >= 0.0f) & (z[u][i] <= 1023.0f);
       }
+      pk = ok;
     }
     pk = __all(pk);
   }
