@@ -1517,8 +1517,9 @@ inline bool row16_fits(const LinArgs& a, int W) {
          stat + static_cast<size_t>(16 * W) * a.ngroups * sizeof(float2) <= 160 * 1024;
 }
 
-// (K splits of the register path on 4097-8192-row layers, 1 < M <= 16:
-// plan::reg4_mid_splits and plan::reg4_wide_splits)
+// (K splits of the register path on 4097-8192-row layers, 1 < M <= 16, and
+// on 3072-4096-row layers, 8 < M <= 16: plan::reg4_mid_splits,
+// plan::reg4_wide_splits and plan::reg4_narrow_splits)
 
 // Large products (M > 16 and enough output tiles): one workgroup per NT x MT
 // tile of (weight rows x activation rows), NT = 128 (K in steps of 64) or 64
@@ -2073,8 +2074,8 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
     // LDS; 3-bit rows are read as dwords (the pitch must keep them aligned)
     if (a.M <= 16 && 64 * a.ngroups * sizeof(float2) <= 64 * 1024 && (BITS == 4 || a.pitch % 4 == 0)) {
       // measured best per shape class (28672 x 4096, 14336 x 4096, 4096 x 14336;
-      // M <= 4 below 8192 rows: 16 waves, 6.7 / 15.8 us against 7.6 / 19.1 us
-      // at 4096 x 4096 / 4096 x 14336)
+      // the 16-wave workgroups below 4097 rows: 6.7 / 15.8 us against 7.6 /
+      // 19.1 us at 4096 x 4096 / 4096 x 14336, M <= 4)
       if (a.N >= 64 * 256) {
         // 241-256 workgroups of 112 rows fill the CUs once where 64-row ones
         // would leave a quarter of them with one workgroup and the rest with
@@ -2103,8 +2104,18 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
         const bool fits = a.part && static_cast<size_t>(s) * a.M * a.N * sizeof(float) <= a.part_bytes;
         return launch_reg4<BITS, 32, 8, BF16>(st, a, s > 1 && fits ? s : 1);
       }
-      if (a.M <= 4) return launch_reg4<BITS, 16, 16, BF16>(st, a);
-      return launch_reg4<BITS, 16, 8, BF16>(st, a);
+      if (const int s = plan::reg4_narrow_splits(a.M, a.N, a.K)) {
+        if (a.part && static_cast<size_t>(s) * a.M * a.N * sizeof(float) <= a.part_bytes)
+          return launch_reg4<BITS, 32, 16, BF16>(st, a, s);
+      }
+      // 16-row workgroups: 16 waves over K, except for 8 < M <= 16 with
+      // K >= 10240 (unsplit there, 8 waves measured 2-3% faster).  Measured
+      // on MI355X against 8 waves (graph-timed, 4-bit, us): M = 8 / 12 / 16 at
+      // 4096 x 4096 6.65 / 7.3 / 7.95 against 7.35 / 7.8 / 8.2, 4096 x 2048
+      // 5.0 / 5.1 / 5.3 against 5.2 / 5.4 / 5.6, M = 5 / 8 at 4096 x 14336
+      // 13.9 / 15.0 against 16.2 / 16.3
+      if (a.M > 8 && a.K >= 10240) return launch_reg4<BITS, 16, 8, BF16>(st, a);
+      return launch_reg4<BITS, 16, 16, BF16>(st, a);
     }
   }
   if constexpr (BITS == 4 || BITS == 3) {

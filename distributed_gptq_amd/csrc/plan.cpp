@@ -148,6 +148,17 @@ int reg4_wide_splits(int64_t M, int64_t N, int64_t K) {
   return M > 1 && M <= 16 && N >= 8192 && ceil_div(N, 64) * 2 <= 256 && N % 4 == 0 && K >= 256 ? 2 : 0;
 }
 
+// 8 < M <= 16 on layers of 3072-4096 rows with K >= 10240: 96-128 workgroups
+// of 32 rows (16 waves), K split in 2.  Measured on MI355X (graph-timed, us,
+// against 16-row workgroups of 8 waves unsplit): 4-bit M = 16 / 12 at 4096 x
+// 14336 16.6 / 15.3 against 19.5 / 17.4, 4096 x 11008 M = 16 14.3 against
+// 16.2, 3584 x 14336 16.6 against 19.8; 3-bit at 4096 x 14336 18.8 / 17.9
+// against 19.7 / 18.2.  At K = 8192 and at M <= 8 it was no faster than the
+// unsplit 16-wave workgroups.
+int reg4_narrow_splits(int64_t M, int64_t N, int64_t K) {
+  return M > 8 && M <= 16 && N >= 3072 && N <= 4096 && N % 4 == 0 && K >= 10240 ? 2 : 0;
+}
+
 size_t round256(size_t b) { return b > SIZE_MAX - 255 ? SIZE_MAX : (b + 255) / 256 * 256; }
 
 size_t splitk_bytes(int64_t M, int64_t N, int64_t K, int bits, int group_size, int x_dtype) {
@@ -158,7 +169,8 @@ size_t splitk_bytes(int64_t M, int64_t N, int64_t K, int bits, int group_size, i
   // M <= 16: the register path stages <= 128 groups per row
   const int sp = M > 16 ? rx_plan(M, N, K, pitch, bits).splits
                         : (bits == 4 || bits == 3) && ceil_div(K, group_size) <= 128
-                              ? std::max(reg4_mid_splits(M, N, K), reg4_wide_splits(M, N, K))
+                              ? std::max({reg4_mid_splits(M, N, K), reg4_wide_splits(M, N, K),
+                                          reg4_narrow_splits(M, N, K)})
                               : 0;
   return sp > 1 ? mul_sat(mul_sat(static_cast<size_t>(sp) * sizeof(float), static_cast<size_t>(M)),
                           static_cast<size_t>(N))

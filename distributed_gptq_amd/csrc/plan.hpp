@@ -70,9 +70,11 @@ struct RxPlan {
 };
 RxPlan rx_plan(int64_t M, int64_t N, int64_t K, int64_t pitch, int bits, bool rows32 = true);
 // K splits of the register path for 1 < M <= 16 on 4097-8191-row layers (0
-// outside these shapes) and on 8192-row layers (0 elsewhere)
+// outside these shapes), on 8192-row layers and, for 8 < M <= 16 with
+// K >= 10240, on 3072-4096-row layers (0 elsewhere)
 int reg4_mid_splits(int64_t M, int64_t N, int64_t K);
 int reg4_wide_splits(int64_t M, int64_t N, int64_t K);
+int reg4_narrow_splits(int64_t M, int64_t N, int64_t K);
 // split-K partial-sum bytes the register kernels use for this layer (0 when
 // they do not split it)
 size_t splitk_bytes(int64_t M, int64_t N, int64_t K, int bits, int group_size, int x_dtype);

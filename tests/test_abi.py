@@ -69,7 +69,13 @@ def test_library_loads_and_reports_version():
     assert h.gptq_linear_workspace_size(64, 4096, 14336, 4, 128, bf16, 0) == 8 * 64 * 4096 * 4
     assert h.gptq_linear_workspace_size(17, 4096, 14336, 3, 128, bf16, 0) == 8 * 17 * 4096 * 4
     assert h.gptq_linear_workspace_size(32, 4096, 4096, 4, 128, bf16, 0) == 0     # M <= 32 on 2^24 weights
-    assert h.gptq_linear_workspace_size(16, 4096, 14336, 4, 128, bf16, 0) == 0    # M <= 16 at 4096 rows
+    # 8 < M <= 16 on 3072-4096 rows with K >= 10240: K in 2 ranges
+    assert h.gptq_linear_workspace_size(16, 4096, 14336, 4, 128, bf16, 0) == 2 * 16 * 4096 * 4
+    assert h.gptq_linear_workspace_size(9, 3072, 10240, 3, 128, bf16, 0) == 2 * 9 * 3072 * 4
+    assert h.gptq_linear_workspace_size(8, 4096, 14336, 4, 128, bf16, 0) == 0     # M <= 8
+    assert h.gptq_linear_workspace_size(16, 4096, 8192, 4, 128, bf16, 0) == 0     # K < 10240
+    assert h.gptq_linear_workspace_size(16, 2048, 14336, 4, 128, bf16, 0) == 0    # < 3072 rows
+    assert h.gptq_linear_workspace_size(16, 4094, 14336, 4, 128, bf16, 0) == 0    # N % 4
     # M > 128: the grid counts two activation tiles (4096 rows: 4 splits)
     assert h.gptq_linear_workspace_size(256, 4096, 4096, 4, 128, bf16, 0) == 4 * 256 * 4096 * 4
     assert h.gptq_linear_workspace_size(256, 28672, 4096, 4, 128, bf16, 0) == 0

@@ -427,6 +427,38 @@ def test_linear_register_mid_rows(hip, xdt, bits, M, N, K, gs):
         check_linear(out, x, codes, scales, zeros, np.arange(K) // gs, bias, bits=bits)
 
 
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bits", [3, 4])
+@pytest.mark.parametrize("M,N,K,gs,split", [
+    (16, 4096, 14336, 128, True),    # 128 workgroups of 32 rows x 2 K ranges
+    (9, 4092, 10240, 128, True),     # M, K at their bounds; last workgroup of 28 rows
+    (12, 3072, 11008, 128, True),    # 86 blocks in two ranges of 43
+    (8, 4096, 14336, 128, False),    # M <= 8: 16-wave workgroups, unsplit
+    (16, 4096, 8192, 128, False),    # K < 10240: 16 waves, unsplit
+    (16, 2048, 14336, 128, False),   # < 3072 rows: 8 waves, unsplit
+    (14, 4094, 14336, 128, False),   # N % 4 != 0: 8 waves, unsplit
+    (6, 4000, 4096, 64, False)])     # groups of 64 (per-weight dequantisation), 16 waves
+def test_linear_register_narrow_rows(hip, xdt, bits, M, N, K, gs, split):
+    """1 < M <= 16 on layers of <= 4096 rows: 16-row workgroups of 16 waves
+    over K, or of 8 waves for 8 < M <= 16 with K >= 10240; on 3072-4096 rows
+    with 8 < M <= 16 and K >= 10240, 32-row workgroups of 16 waves with K in
+    2 ranges (partials reduced in order, bias added there) when the workspace
+    holds the partials, else the 8-wave workgroups.  Through gptq_linear_ws and
+    gptq_linear (no workspace), against the fp64 oracle; repeated calls are
+    bit-identical."""
+    from distributed_gptq_amd import _lib, _ops
+    nb = _lib.lib().gptq_linear_workspace_size(M, N, K, bits, gs, _ops.dtype_code(xdt), 0)
+    assert nb == (2 * M * N * 4 if split else 0)
+    codes, scales, zeros, x = _case(M, N, K, bits, gs, M + N + K + bits + 7, xdt)
+    bias = torch.randn(N).to(xdt)
+    packed = torch.from_numpy(O.pack_bitstream(codes, bits)).cuda()
+    args = (x.cuda(), packed, bits, scales.cuda(), zeros.cuda(), K)
+    y = _ops.linear(*args, group_size=gs, bias=bias.cuda())
+    assert torch.equal(y, _ops.linear(*args, group_size=gs, bias=bias.cuda()))
+    for out in (y, _linear_plain(*args, gs, bias.cuda())):
+        check_linear(out, x, codes, scales, zeros, np.arange(K) // gs, bias, bits=bits)
+
+
 def test_linear_ws_workspace_alignment_and_size(hip):
     """gptq_linear_ws with a workspace that starts 4 bytes past a 256-byte
     boundary: the partial sums start at the next boundary, so the exact size
