@@ -2097,6 +2097,11 @@ int launch_dq_gemm(hipStream_t st, const LinArgs& a) {
       }
       if (a.N >= 32 * 256) {
         const int s = plan::reg4_wide_splits(a.M, a.N, a.K);
+        // 8193-16383 rows at M <= 4: 32-row workgroups (measured on MI355X,
+        // graph-timed, 4-bit M = 2, us: 14336 x 4096 11.3 against 12.0 with 64
+        // rows, 11008 x 4096 11.0 against 11.6, 13824 x 5120 14.0 against 15.9;
+        // 3-bit 3-4% faster; at M = 8 and 16 the 64-row workgroups stay faster)
+        if (s == 0 && a.M <= 4) return launch_reg4<BITS, 32, 8, BF16>(st, a);
         const bool fits = s > 1 && a.part && static_cast<size_t>(s) * a.M * a.N * sizeof(float) <= a.part_bytes;
         return launch_reg4<BITS, 64, 8, BF16>(st, a, fits ? s : 1);
       }

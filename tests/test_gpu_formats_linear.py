@@ -514,13 +514,14 @@ def test_linear_scales_at_odd_offset(hip, xdt, M, N):
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("bits", [2, 3, 4, 8])
 @pytest.mark.parametrize("gs", [128, 32])
-@pytest.mark.parametrize("M,N", [(2, 8192 + 37), (4, 8192 + 37), (16, 8192 + 37),
+@pytest.mark.parametrize("M,N", [(2, 8192 + 37), (4, 8192 + 37), (16, 8192 + 37), (3, 14336 - 20),
                                  (2, 16384 + 5), (4, 16384 + 5), (16, 16384 + 5)])
 def test_linear_small_m_wide_n(hip, xdt, bits, gs, M, N):
-    """M <= 16 with N >= 8192 and >= 16384: the 64-row register kernels
-    (3/4-bit: dq_reg4_k with 8 and 4 waves) and the wide split-K kernels
-    (2/8-bit), ragged N (the last tile's clamp), with groups of 128 (zero
-    points folded per block) and 32 (dequantised per weight)."""
+    """M <= 16 with N >= 8192 and >= 16384: the register kernels (3/4-bit:
+    dq_reg4_k with 64-row workgroups of 8 and 4 waves, and 32-row ones for
+    M <= 4 below 16384 rows) and the wide split-K kernels (2/8-bit), ragged
+    N (the last tile's clamp), with groups of 128 (zero points folded per
+    block) and 32 (dequantised per weight)."""
     from distributed_gptq_amd import _ops
     K = 1024
     codes, scales, zeros, x = _case(M, N, K, bits, gs, M + N + bits + gs, xdt)
