@@ -1847,8 +1847,8 @@ __global__ __launch_bounds__(64 * (WAVES + L)) __attribute__((amdgpu_waves_per_e
       // fp16 zeros (pk requires them); the check combines with `&`, not
       // `&&`: a short-circuit let the compiler load each zero only after the
       // previous one passed, a chain of 8 NB dependent loads with 32 rows per
-      // wave (the same time at the Llama-3-8B layer shapes, where they hit the cache;
-      // now one round trip whatever the cache holds)
+      // wave (the same time at the Llama-3-8B layer shapes, where the zeros
+      // hit the cache; now one round trip whatever the cache holds)
       const _Float16* zh = static_cast<const _Float16*>(a.zeros);
       bool ok = true;
       for (int64_t g0 = g_lo + g4; g0 < g_hi; g0 += 32) {
