@@ -256,17 +256,19 @@ def run_block(args, torch, F, dev):
     breakdown = {k: round(sum(r[k] for r in recs) / len(recs), 3) for k in ("forward_ms", "hessian_ms", "quantize_ms")}
     losses = {k: float(v.losses_sum.item()) for k, v in res.items()}
     # the dominant kernel alone: the down_proj Hessian over all tokens (the
-    # block's own calibration data), timed on its stream
+    # block's own calibration data), timed on its stream: the mean of three
+    # launch pairs after one untimed
     iso = []
-    for _ in range(2):
+    for i in range(4):
         a, b = ev(), ev()
         Hs[first].zero_()
         a.record()
         _ops.hessian_accumulate(Hs[first], bufs[first])
         b.record()
         torch.cuda.synchronize()
-        iso.append(a.elapsed_time(b))
-    iso_ms = min(iso)
+        if i:
+            iso.append(a.elapsed_time(b))
+    iso_ms = sum(iso) / len(iso)
     iso_flops = hessian_flops(n, bufs[first].shape[1])
     iso_bytes = n * bufs[first].shape[1] * 2 + 2 * bufs[first].shape[1] ** 2 * 4
     del bufs, Hs, z
