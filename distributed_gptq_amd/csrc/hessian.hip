@@ -747,7 +747,9 @@ __global__ __launch_bounds__(256) void hessian_reduce(float* __restrict__ H, int
   const int64_t gi = static_cast<int64_t>(I) * kTile + sr * 32 + row;
   const int64_t tstride = static_cast<int64_t>(ntiles) * kTile * kTile;
   const float* p = partial + static_cast<int64_t>(tile) * kTile * kTile + (sr * 32 + row) * kTile + sc * 32 + col0;
-  // partials summed in split order; eight loads are issued before their adds
+  // partials summed in split order; up to eight loads are issued before
+  // their adds (the last < 8 as well: one at a time, each waited for, they
+  // were a chain of round trips with 4 splits)
   f32x4 v = *reinterpret_cast<const f32x4*>(p);
   int s = 1;
   for (; s + 8 <= S; s += 8) {
@@ -757,13 +759,32 @@ __global__ __launch_bounds__(256) void hessian_reduce(float* __restrict__ H, int
 #pragma unroll
     for (int u = 0; u < 8; ++u) v += w[u];
   }
-  for (; s < S; ++s) v += *reinterpret_cast<const f32x4*>(p + s * tstride);
+  if (s < S) {
+    f32x4 w[7];
+#pragma unroll
+    for (int u = 0; u < 7; ++u)
+      if (s + u < S) w[u] = *reinterpret_cast<const f32x4*>(p + (s + u) * tstride);
+#pragma unroll
+    for (int u = 0; u < 7; ++u)
+      if (s + u < S) v += w[u];
+  }
+  // H's four elements read together (one 16-byte load when the quad is in
+  // bounds), before any is added or written
+  const int64_t gj0 = static_cast<int64_t>(J) * kTile + sc * 32 + col0;
+  f32x4 hv = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (gi < K && gj0 + 3 < K && (K & 3) == 0) {
+    hv = *reinterpret_cast<const f32x4*>(H + gi * K + gj0);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (gi < K && gj0 + e < K) hv[e] = H[gi * K + gj0 + e];
+  }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const int64_t gj = static_cast<int64_t>(J) * kTile + sc * 32 + col0 + e;
+    const int64_t gj = gj0 + e;
     float val = v[e];
     if (gi < K && gj < K) {
-      val += H[gi * K + gj];
+      val += hv[e];
       if (!diag_sb || gi >= gj) H[gi * K + gj] = val;
     }
     t[row][col0 + e] = val;
