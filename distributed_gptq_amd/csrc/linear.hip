@@ -1295,14 +1295,45 @@ __global__ __launch_bounds__(256) void splitk_reduce_k(const float* __restrict__
   const int64_t e = 4 * q;
   if (e >= M * N) return;
   const int64_t plane = M * N;
+  // partials added in split order, up to eight loads in flight before their
+  // adds (one load and wait per split was S - 1 round trips in a row; the
+  // call measured the same in HIP graphs, where the reduce's launch and its
+  // traffic dominate), the quad's four outputs in one store
   f32x4 v = *reinterpret_cast<const f32x4*>(part + e);
-  for (int s = 1; s < S; ++s) v += *reinterpret_cast<const f32x4*>(part + s * plane + e);
-  const int64_t n = e % N;
+  int s = 1;
+  for (; s + 8 <= S; s += 8) {
+    f32x4 w[8];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    float r = v[u];
-    if (bias) r += load_elem(bias, n + u, bias_dtype);
-    store_elem(y, e + u, y_dtype, r);
+    for (int u = 0; u < 8; ++u) w[u] = *reinterpret_cast<const f32x4*>(part + (s + u) * plane + e);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v += w[u];
+  }
+  if (s < S) {
+    f32x4 w[7];
+#pragma unroll
+    for (int u = 0; u < 7; ++u)
+      if (s + u < S) w[u] = *reinterpret_cast<const f32x4*>(part + (s + u) * plane + e);
+#pragma unroll
+    for (int u = 0; u < 7; ++u)
+      if (s + u < S) v += w[u];
+  }
+  const int64_t n = e % N;  // N % 4 == 0: the quad lies in one row
+  float r[4] = {v[0], v[1], v[2], v[3]};
+  if (bias) {
+    float b[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) b[u] = load_elem(bias, n + u, bias_dtype);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) r[u] += b[u];
+  }
+  if (y_dtype != GPTQ_F32 && (reinterpret_cast<uintptr_t>(y) & 7) == 0) {
+    uint32_t h[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) h[u] = y_dtype == GPTQ_BF16 ? f32_to_bf16_bits(r[u]) : f32_to_f16_bits(r[u]);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(y) + e) = uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+  } else {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) store_elem(y, e + u, y_dtype, r[u]);
   }
 }
 
